@@ -1,0 +1,155 @@
+/* libmstar_moe -- C-ABI of the MI355X (gfx950) fused Mixture-of-Experts path.
+ *
+ * Conventions for every entry point
+ *   - All tensor arguments are device pointers owned by the caller.  No entry
+ *     point allocates, frees or synchronises; work is enqueued on `stream`
+ *     (a hipStream_t; NULL means the default stream of the current device).
+ *   - Return value: 0 on success, otherwise an MSTAR_* status code.  The
+ *     message of the calling thread's last failure is returned by
+ *     mstar_moe_last_error().  No C++ exception crosses this boundary.
+ *   - Dtype codes: MSTAR_DTYPE_*.  Tensors are dense, row-major, contiguous.
+ *   - Launches are graph-capturable: no host reads of device data, all grid
+ *     sizes follow from the arguments (never from routing results).
+ *
+ * Reference citations are `file:line` in mstar-project/mstar.
+ */
+#ifndef MSTAR_MOE_H_
+#define MSTAR_MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSTAR_MOE_ABI_VERSION 1
+
+/* status codes */
+#define MSTAR_OK 0
+#define MSTAR_INVALID_ARGUMENT 1
+#define MSTAR_UNSUPPORTED 2
+#define MSTAR_LAUNCH_ERROR 3
+#define MSTAR_WORKSPACE_TOO_SMALL 4
+
+/* dtype codes */
+#define MSTAR_DTYPE_F32 0
+#define MSTAR_DTYPE_BF16 1
+#define MSTAR_DTYPE_F16 2
+#define MSTAR_DTYPE_I32 3
+#define MSTAR_DTYPE_I64 4
+#define MSTAR_DTYPE_FP8_E4M3FN 5
+
+/* quantisation modes of mstar_fused_moe */
+#define MSTAR_QUANT_NONE 0     /* w1/w2 in the activation dtype (bf16/fp16)          */
+#define MSTAR_QUANT_FP8_W8A8 1 /* e4m3fn weights, 128x128 block scales; activations   */
+                               /* quantised per token-group of 128 inside the call    */
+#define MSTAR_QUANT_W4A16 2    /* int4 weights (u = q + 8, 8 per int32, element k in  */
+                               /* bits 4*(k%8) of word k/8), bf16 scales per 128 of K */
+
+/* Message for the calling thread's most recent failure ("" if none). */
+const char* mstar_moe_last_error(void);
+int mstar_moe_abi_version(void);
+
+/* Softmax top-k routing from router logits.
+ * Replaces TopKRouter.forward from the logits on
+ * (mstar/model/components/moe.py:131-139): fp32 softmax, top-k (ties go to
+ * the lower expert index), optional renormalisation (norm_topk_prob).
+ * logits [num_tokens, num_experts] fp32 or bf16 -> topk_weights
+ * [num_tokens, top_k] fp32 and ids as int32 and/or int64 (either may be NULL,
+ * not both).  num_experts <= 1024, top_k <= 64. */
+int mstar_moe_topk_softmax(const void* logits, int logits_dtype, int64_t num_tokens,
+                           int num_experts, int top_k, int renormalize, float* topk_weights,
+                           int32_t* topk_ids_i32, int64_t* topk_ids_i64, void* stream);
+
+/* Token permutation into expert-aligned blocks.
+ * Replaces torch.ops._mstar_moe_C.moe_align_block_size
+ * (mstar/utils/fused_moe/csrc/moe_align_block_size.cu:207-282) as called by
+ * moe_align_block_size (mstar/utils/fused_moe/align.py:55-103).  Same
+ * outputs: sorted_token_ids [sorted_len] (padding = numel), expert_ids
+ * [expert_ids_len] (blocks past the end = 0), num_tokens_post_pad [1].  The
+ * order inside an expert is ascending slot index (the stable order of
+ * align.py:146).  Optional extras: expert_offsets [E+1] (padded starts) and
+ * expert_counts [E] (unpadded).  Same errors as the reference: padded
+ * expert count must be < 1024 (moe_align_block_size.cu:223). */
+int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
+                               int num_experts, int block_size, int32_t* sorted_token_ids,
+                               int64_t sorted_len, int32_t* expert_ids, int64_t expert_ids_len,
+                               int32_t* num_tokens_post_pad, int32_t* expert_offsets,
+                               int32_t* expert_counts, void* stream);
+
+/* out[r, :] = dt(dt(act_f32(gate_up[r, :I])) * gate_up[r, I:]).
+ * Replaces act_and_mul_triton (mstar/utils/fused_moe/kernels.py:279-298).
+ * activation: 0 = silu, 1 = gelu (tanh). */
+int mstar_moe_act_and_mul(const void* gate_up, void* out, int dtype, int64_t rows, int64_t inter,
+                          int activation, void* stream);
+
+/* output[t, :] = dt(scale * sum_j fp32(input[t, j, :])).
+ * Replaces moe_sum_reduce_triton (mstar/utils/fused_moe/kernels.py:359-393). */
+int mstar_moe_sum_reduce(const void* input, void* output, int dtype, int64_t tokens,
+                         int64_t top_k, int64_t hidden, float routed_scaling_factor,
+                         void* stream);
+
+/* Grouped GEMM over expert-aligned blocks, bf16/fp16 (no quantisation):
+ * C[slot, :] = dt(A[slot / top_k, :] . B[e(slot)]^T (* topk_weights[slot])).
+ * Replaces invoke_fused_moe_kernel / fused_moe_kernel
+ * (mstar/utils/fused_moe/kernels.py:141-218, 36-138).  block_size must be
+ * the one given to mstar_moe_align_block_size (16, 32, 64 or 128);
+ * K % 128 == 0.  em = sorted_len. */
+int mstar_moe_grouped_gemm(const void* A, const void* B, void* C, const void* topk_weights,
+                           int topk_w_dtype, const int32_t* sorted_token_ids,
+                           const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                           int64_t N, int64_t K, int64_t em, int64_t num_valid_tokens, int top_k,
+                           int mul_routed_weight, int block_size, int dtype, void* stream);
+
+/* Workspace bytes mstar_fused_moe needs for these sizes. */
+int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
+                                   int64_t inter, int top_k, int quant, int act_dtype,
+                                   int reduce_results, size_t* bytes);
+
+/* The whole routed-expert computation: align -> gate_up GEMM (+ fused
+ * SiLU-and-mul) -> down GEMM (x routed weight) -> top-k sum.
+ * Replaces fused_experts (mstar/utils/fused_moe/runner.py:31-159) and its
+ * callers' naive fallback dispatch_experts_fused
+ * (mstar/model/components/moe.py:143-185).
+ *   hidden [num_tokens, hidden_size]; w1 [E, 2*inter, hidden_size] rows
+ *   [gate; up]; w2 [E, hidden_size, inter];
+ *   quant = MSTAR_QUANT_FP8_W8A8: w1/w2 e4m3fn, w1_scale fp32
+ *     [E, 2*inter/128, hidden/128], w2_scale fp32 [E, hidden/128, inter/128];
+ *   quant = MSTAR_QUANT_W4A16: w1 int32 [E, 2*inter, hidden/8], w1_scale bf16
+ *     [E, 2*inter, hidden/128]; w2 int32 [E, hidden, inter/8], w2_scale bf16
+ *     [E, hidden, inter/128];
+ *   topk_weights [num_tokens, top_k] fp32/bf16/fp16; topk_ids int32/int64;
+ *   out [num_tokens, hidden_size], or [num_tokens, top_k, hidden_size] when
+ *   reduce_results == 0 (runner.py:155-156).
+ * hidden_size and inter must be multiples of 128. */
+int mstar_fused_moe(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                    const void* w1, const void* w2, int num_experts, int64_t inter, int quant,
+                    const void* w1_scale, const void* w2_scale, const void* topk_weights,
+                    int topk_w_dtype, const void* topk_ids, int ids_dtype, int top_k,
+                    int activation, int reduce_results, void* out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* Activation quantisation, OCP e4m3fn: per token-group of 128
+ * (s = max(amax, 1e-10) / 448, scales [rows, cols/128]) or per token
+ * (scales [rows]).  No reference counterpart: the reference's FP8 branches
+ * were stripped (mstar/utils/fused_moe/kernels.py:3-7); these produce the
+ * activation formats of BASELINE configs 2-4. */
+int mstar_quant_fp8_per_token_group(const void* x, int dtype, int64_t rows, int64_t cols,
+                                    int group_size, uint8_t* q, float* scales, void* stream);
+int mstar_quant_fp8_per_token(const void* x, int dtype, int64_t rows, int64_t cols, uint8_t* q,
+                              float* scales, void* stream);
+
+/* out[M, N] bf16 = (a[M, K] . w[N, K]^T) * a_scale[m] * w_scale[n], e4m3fn
+ * operands, fp32 accumulation.  Replaces the F.linear of the dense layers
+ * (mstar/model/components/distributed/linear.py:101, :412;
+ * mstar/model/components/linear.py:94) for W8A8 weights.  K % 128 == 0. */
+int mstar_fp8_scaled_mm(const uint8_t* a, const float* a_scale, const uint8_t* w,
+                        const float* w_scale, void* out, int64_t M, int64_t N, int64_t K,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSTAR_MOE_H_ */

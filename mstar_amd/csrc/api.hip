@@ -1,0 +1,321 @@
+// C-ABI of libmstar_moe: plain pointers, sizes and a stream handle.
+//
+// Rules for every entry point: the caller owns all buffers (device memory,
+// already allocated); nothing here allocates or synchronises; work is
+// enqueued on the stream passed in (NULL = the default stream of the current
+// device); the return value is 0 or a status code, and
+// mstar_moe_last_error() describes the last failure of the calling thread.
+// The declarations, with the reference interface each one replaces, are in
+// include/mstar_moe.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+#include "launch.h"
+#include "../../include/mstar_moe.h"
+
+namespace mstar {
+
+static thread_local char g_last_error[512] = "";
+
+void set_last_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_last_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return kLaunchError;
+  }
+  return kOk;
+}
+
+static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Row block for the tiled grouped GEMM: about one block per expert's share of
+// the slots, so padding stays a small fraction of the work.
+static int choose_bm(int64_t slots, int E) {
+  const int64_t avg = slots / (E > 0 ? E : 1);
+  if (avg <= 48) return 32;
+  if (avg <= 160) return 64;
+  return 128;
+}
+
+// Largest token count served by the weight-streaming kernels.
+constexpr int64_t kStreamMaxTokens = 64;
+
+struct Plan {
+  bool stream = false;
+  int bm = 16;
+  int64_t slots = 0, max_padded = 0, max_blocks = 0;
+  size_t off_sorted, off_eids, off_ntpp, off_eoff, off_ecnt, off_c2, off_c3, off_hq, off_hs,
+      off_cq, off_cs, total;
+};
+
+static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quant, int act_dtype,
+                     int reduce, Plan* pl) {
+  if (M < 0 || H <= 0 || E <= 0 || I <= 0 || top_k <= 0 || top_k > E) {
+    set_last_error("fused_moe: invalid sizes (M=%lld H=%lld E=%d I=%lld top_k=%d)",
+                   (long long)M, (long long)H, E, (long long)I, top_k);
+    return kInvalidArgument;
+  }
+  if (H % 128 != 0 || I % 128 != 0) {
+    set_last_error("fused_moe: hidden and intermediate sizes must be multiples of 128 "
+                   "(H=%lld I=%lld)", (long long)H, (long long)I);
+    return kUnsupported;
+  }
+  if (quant != MSTAR_QUANT_NONE && act_dtype != kBF16) {
+    set_last_error("fused_moe: quantised paths take bf16 activations");
+    return kUnsupported;
+  }
+  if (act_dtype != kBF16 && act_dtype != kF16) {
+    set_last_error("fused_moe: activations must be bf16 or fp16");
+    return kUnsupported;
+  }
+  pl->slots = M * top_k;
+  const int bkind = quant == MSTAR_QUANT_FP8_W8A8 ? B_FP8BLK : quant == MSTAR_QUANT_W4A16 ? B_INT4G : B_H16;
+  pl->stream = quant != MSTAR_QUANT_NONE && M <= kStreamMaxTokens &&
+               stream_gemm_supported((int)H, (int)M, A_H16, bkind) &&
+               stream_gemm_supported((int)I, (int)M, A_H16, bkind);
+  pl->bm = pl->stream ? 16 : choose_bm(pl->slots, E);
+  pl->max_padded = pl->slots + (int64_t)E * (pl->bm - 1);
+  pl->max_blocks = (pl->max_padded + pl->bm - 1) / pl->bm;
+  size_t o = 0;
+  auto take = [&](size_t bytes) { size_t r = o; o = align_up(o + bytes); return r; };
+  pl->off_sorted = take(pl->max_padded * 4);
+  pl->off_eids = take(pl->max_blocks * 4);
+  pl->off_ntpp = take(4);
+  pl->off_eoff = take((size_t)(E + 1) * 4);
+  pl->off_ecnt = take((size_t)E * 4);
+  pl->off_c2 = take((size_t)pl->slots * I * 2);
+  pl->off_c3 = reduce ? take((size_t)pl->slots * H * 2) : 0;
+  const bool fp8_tiled = quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream;
+  pl->off_hq = fp8_tiled ? take((size_t)M * H) : 0;
+  pl->off_hs = fp8_tiled ? take((size_t)M * (H / 128) * 4) : 0;
+  pl->off_cq = fp8_tiled ? take((size_t)pl->slots * I) : 0;
+  pl->off_cs = fp8_tiled ? take((size_t)pl->slots * (I / 128) * 4) : 0;
+  pl->total = o;
+  return kOk;
+}
+
+}  // namespace mstar
+
+using namespace mstar;
+
+extern "C" {
+
+const char* mstar_moe_last_error(void) { return g_last_error; }
+
+int mstar_moe_abi_version(void) { return MSTAR_MOE_ABI_VERSION; }
+
+int mstar_moe_topk_softmax(const void* logits, int logits_dtype, int64_t num_tokens,
+                           int num_experts, int top_k, int renormalize, float* topk_weights,
+                           int32_t* topk_ids_i32, int64_t* topk_ids_i64, void* stream) {
+  return launch_topk_softmax(logits, logits_dtype, num_tokens, num_experts, top_k, renormalize,
+                             topk_weights, topk_ids_i32, topk_ids_i64, (hipStream_t)stream);
+}
+
+int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
+                               int num_experts, int block_size, int32_t* sorted_token_ids,
+                               int64_t sorted_len, int32_t* expert_ids, int64_t expert_ids_len,
+                               int32_t* num_tokens_post_pad, int32_t* expert_offsets,
+                               int32_t* expert_counts, void* stream) {
+  if (block_size > 0 && expert_ids_len < (sorted_len + block_size - 1) / block_size) {
+    set_last_error("moe_align_block_size: experts_ids too small (%lld < %lld)",
+                   (long long)expert_ids_len,
+                   (long long)((sorted_len + block_size - 1) / block_size));
+    return kInvalidArgument;
+  }
+  return launch_align(topk_ids, ids_dtype, numel, num_experts, block_size, sorted_token_ids,
+                      expert_ids, num_tokens_post_pad, sorted_len, expert_offsets, expert_counts,
+                      (hipStream_t)stream);
+}
+
+int mstar_moe_act_and_mul(const void* gate_up, void* out, int dtype, int64_t rows, int64_t inter,
+                          int activation, void* stream) {
+  return launch_act_and_mul(gate_up, out, dtype, rows, inter, activation, (hipStream_t)stream);
+}
+
+int mstar_moe_sum_reduce(const void* input, void* output, int dtype, int64_t tokens,
+                         int64_t top_k, int64_t hidden, float routed_scaling_factor,
+                         void* stream) {
+  return launch_sum_reduce(input, output, dtype, tokens, top_k, hidden, routed_scaling_factor,
+                           (hipStream_t)stream);
+}
+
+int mstar_quant_fp8_per_token_group(const void* x, int dtype, int64_t rows, int64_t cols,
+                                    int group_size, uint8_t* q, float* scales, void* stream) {
+  if (group_size != 128) {
+    set_last_error("quant_fp8_per_token_group: only group_size 128 is supported");
+    return kUnsupported;
+  }
+  return launch_quant_fp8_group(x, dtype, rows, cols, cols, q, scales, (hipStream_t)stream);
+}
+
+int mstar_quant_fp8_per_token(const void* x, int dtype, int64_t rows, int64_t cols, uint8_t* q,
+                              float* scales, void* stream) {
+  return launch_quant_fp8_row(x, dtype, rows, cols, q, scales, (hipStream_t)stream);
+}
+
+int mstar_fp8_scaled_mm(const uint8_t* a, const float* a_scale, const uint8_t* w,
+                        const float* w_scale, void* out, int64_t M, int64_t N, int64_t K,
+                        void* stream) {
+  if (M < 0 || N <= 0 || K <= 0 || N >= (1ll << 31) || K % 128 != 0 || !out ||
+      (M > 0 && (!a || !a_scale || !w || !w_scale))) {
+    set_last_error("fp8_scaled_mm: invalid arguments (M=%lld N=%lld K=%lld; K %% 128 == 0)",
+                   (long long)M, (long long)N, (long long)K);
+    return kInvalidArgument;
+  }
+  if (M == 0) return kOk;
+  GemmArgs g = {};
+  g.A = a; g.lda = K; g.a_scale = a_scale;
+  g.B = w; g.ldb = K; g.b_estride = 0; g.b_scale = w_scale;
+  g.C = out; g.ldc = N;
+  g.M = M; g.N = (int)N; g.K = (int)K; g.top_k = 1;
+  const int bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+  return launch_tile_gemm(g, A_FP8R, B_FP8R, EPI_DENSE, kBF16, false, bm, (hipStream_t)stream);
+}
+
+int mstar_moe_grouped_gemm(const void* A, const void* B, void* C, const void* topk_weights,
+                           int topk_w_dtype, const int32_t* sorted_token_ids,
+                           const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                           int64_t N, int64_t K, int64_t em, int64_t num_valid_tokens, int top_k,
+                           int mul_routed_weight, int block_size, int dtype, void* stream) {
+  if (N <= 0 || K <= 0 || em < 0 || top_k <= 0 || !A || !B || !C || !sorted_token_ids ||
+      !expert_ids || !num_tokens_post_padded || (mul_routed_weight && !topk_weights)) {
+    set_last_error("moe_grouped_gemm: invalid arguments");
+    return kInvalidArgument;
+  }
+  GemmArgs g = {};
+  g.A = A; g.lda = K;
+  g.B = B; g.ldb = K; g.b_estride = N * K;
+  g.C = C; g.ldc = N;
+  g.topk_w = topk_weights; g.topk_w_dtype = topk_w_dtype;
+  g.sorted_ids = sorted_token_ids; g.expert_ids = expert_ids; g.ntpp = num_tokens_post_padded;
+  g.M = num_valid_tokens; g.N = (int)N; g.K = (int)K; g.top_k = top_k;
+  g.mul_routed = mul_routed_weight;
+  g.m_blocks = (int)((em + block_size - 1) / block_size);
+  return launch_tile_gemm(g, A_H16, B_H16, EPI_STORE, dtype, true, block_size,
+                          (hipStream_t)stream);
+}
+
+int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
+                                   int64_t inter, int top_k, int quant, int act_dtype,
+                                   int reduce_results, size_t* bytes) {
+  Plan pl;
+  int st = make_plan(num_tokens, hidden, num_experts, inter, top_k, quant, act_dtype,
+                     reduce_results, &pl);
+  if (st == kOk && bytes) *bytes = pl.total;
+  return st;
+}
+
+int mstar_fused_moe(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                    const void* w1, const void* w2, int num_experts, int64_t inter, int quant,
+                    const void* w1_scale, const void* w2_scale, const void* topk_weights,
+                    int topk_w_dtype, const void* topk_ids, int ids_dtype, int top_k,
+                    int activation, int reduce_results, void* out, void* workspace,
+                    size_t workspace_bytes, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  Plan pl;
+  int st = make_plan(num_tokens, hidden_size, num_experts, inter, top_k, quant, act_dtype,
+                     reduce_results, &pl);
+  if (st != kOk) return st;
+  if (activation != 0 && activation != 1) {
+    set_last_error("fused_moe: activation must be 0 (silu) or 1 (gelu)");
+    return kInvalidArgument;
+  }
+  if (workspace_bytes < pl.total || (pl.total > 0 && !workspace)) {
+    set_last_error("fused_moe: workspace too small (%zu < %zu)", workspace_bytes, pl.total);
+    return kWorkspaceTooSmall;
+  }
+  if (num_tokens == 0) return kOk;
+  if (!hidden || !w1 || !w2 || !topk_weights || !topk_ids || !out ||
+      (quant != MSTAR_QUANT_NONE && (!w1_scale || !w2_scale))) {
+    set_last_error("fused_moe: null tensor pointer");
+    return kInvalidArgument;
+  }
+  const int64_t M = num_tokens, H = hidden_size, I = inter;
+  const int E = num_experts;
+  uint8_t* ws = (uint8_t*)workspace;
+  int32_t* sorted = (int32_t*)(ws + pl.off_sorted);
+  int32_t* eids = (int32_t*)(ws + pl.off_eids);
+  int32_t* ntpp = (int32_t*)(ws + pl.off_ntpp);
+  int32_t* eoff = (int32_t*)(ws + pl.off_eoff);
+  int32_t* ecnt = (int32_t*)(ws + pl.off_ecnt);
+  void* cache2 = ws + pl.off_c2;
+  void* cache3 = reduce_results ? (void*)(ws + pl.off_c3) : out;
+
+  st = launch_align(topk_ids, ids_dtype, pl.slots, E, pl.bm, sorted, eids, ntpp, pl.max_padded,
+                    eoff, ecnt, stream);
+  if (st != kOk) return st;
+
+  const int bkind = quant == MSTAR_QUANT_FP8_W8A8 ? B_FP8BLK : quant == MSTAR_QUANT_W4A16 ? B_INT4G : B_H16;
+  GemmArgs g1 = {};
+  g1.B = w1;
+  g1.C = cache2; g1.ldc = I;
+  g1.sorted_ids = sorted; g1.expert_ids = eids; g1.ntpp = ntpp;
+  g1.expert_off = eoff; g1.expert_cnt = ecnt;
+  g1.M = pl.slots; g1.N = (int)(2 * I); g1.K = (int)H; g1.top_k = top_k; g1.inter = (int)I;
+  g1.activation = activation; g1.num_experts = E; g1.m_blocks = (int)pl.max_blocks;
+  g1.topk_w = topk_weights; g1.topk_w_dtype = topk_w_dtype;
+  GemmArgs g2 = g1;
+  g2.B = w2;
+  g2.C = cache3; g2.ldc = H;
+  g2.N = (int)H; g2.K = (int)I; g2.top_k = 1; g2.mul_routed = 1;
+  g2.A = cache2; g2.lda = I;
+
+  if (bkind == B_FP8BLK) {
+    // w1: [E][2I][H] e4m3fn, scales [E][2I/128][H/128]; w2: [E][H][I], [E][H/128][I/128].
+    g1.ldb = H; g1.b_estride = 2 * I * H; g1.b_scale = w1_scale;
+    g1.bs_ld = H / 128; g1.bs_estride = (2 * I / 128) * (H / 128);
+    g2.ldb = I; g2.b_estride = H * I; g2.b_scale = w2_scale;
+    g2.bs_ld = I / 128; g2.bs_estride = (H / 128) * (I / 128);
+  } else if (bkind == B_INT4G) {
+    // w1: [E][2I][H/8] int32, scales [E][2I][H/128] bf16; w2: [E][H][I/8], [E][H][I/128].
+    g1.ldb = H / 8; g1.b_estride = 2 * I * (H / 8); g1.b_scale = w1_scale;
+    g1.bs_ld = H / 128; g1.bs_estride = 2 * I * (H / 128);
+    g2.ldb = I / 8; g2.b_estride = H * (I / 8); g2.b_scale = w2_scale;
+    g2.bs_ld = I / 128; g2.bs_estride = H * (I / 128);
+  } else {
+    g1.ldb = H; g1.b_estride = 2 * I * H;
+    g2.ldb = I; g2.b_estride = H * I;
+  }
+
+  if (pl.stream) {
+    g1.A = hidden; g1.lda = H;
+    st = launch_stream_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, (int)M, stream);
+    if (st != kOk) return st;
+    st = launch_stream_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, (int)M, stream);
+    if (st != kOk) return st;
+  } else if (bkind == B_FP8BLK) {
+    uint8_t* hq = ws + pl.off_hq;
+    float* hs = (float*)(ws + pl.off_hs);
+    uint8_t* cq = ws + pl.off_cq;
+    float* cs = (float*)(ws + pl.off_cs);
+    st = launch_quant_fp8_group(hidden, act_dtype, M, H, H, hq, hs, stream);
+    if (st != kOk) return st;
+    g1.A = hq; g1.lda = H; g1.a_scale = hs; g1.ld_as = H / 128;
+    st = launch_tile_gemm(g1, A_FP8G, B_FP8BLK, EPI_ACT, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+    st = launch_quant_fp8_group(cache2, act_dtype, pl.slots, I, I, cq, cs, stream);
+    if (st != kOk) return st;
+    g2.A = cq; g2.lda = I; g2.a_scale = cs; g2.ld_as = I / 128;
+    st = launch_tile_gemm(g2, A_FP8G, B_FP8BLK, EPI_STORE, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+  } else {
+    g1.A = hidden; g1.lda = H;
+    st = launch_tile_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+    st = launch_tile_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+  }
+  if (reduce_results)
+    return launch_sum_reduce(cache3, out, act_dtype, M, top_k, H, 1.0f, stream);
+  return kOk;
+}
+
+}  // extern "C"

@@ -1,0 +1,153 @@
+// Shared device helpers for the gfx950 fused-MoE kernels.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, the
+// OCP e4m3fn FP8 format (not the fnuz variant of gfx942) and the CDNA4
+// MFMA instructions v_mfma_f32_16x16x128_f8f6f4 / v_mfma_f32_16x16x32_bf16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mstar {
+
+// ---------------------------------------------------------------- status codes
+enum Status : int {
+  kOk = 0,
+  kInvalidArgument = 1,
+  kUnsupported = 2,
+  kLaunchError = 3,
+  kWorkspaceTooSmall = 4,
+};
+
+void set_last_error(const char* fmt, ...);
+int launch_status(const char* what);
+
+// ------------------------------------------------------------- element types
+enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2, kI32 = 3, kI64 = 4, kFP8 = 5 };
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+constexpr float kFp8Max = 448.0f;
+constexpr float kQuantEps = 1e-10f;
+
+// bf16 <-> f32 with round-to-nearest-even, matching torch's float->bfloat16.
+__device__ __host__ inline uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __host__ inline float bf16_bits_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+__device__ inline float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ inline float f16_bits_to_f32(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// 16-bit activation type tag: 1 = bf16, 2 = fp16.
+template <int DT>
+__device__ inline float h16_to_f32(uint16_t b) {
+  if constexpr (DT == kBF16) return bf16_bits_to_f32(b);
+  else return f16_bits_to_f32(b);
+}
+template <int DT>
+__device__ inline uint16_t f32_to_h16(float f) {
+  if constexpr (DT == kBF16) return f32_to_bf16_bits(f);
+  else return f32_to_f16_bits(f);
+}
+template <int DT>
+__device__ inline float round_h16(float f) { return h16_to_f32<DT>(f32_to_h16<DT>(f)); }
+
+// Two floats -> two OCP e4m3fn bytes (RNE, inputs already clamped to +-448),
+// packed into the low (hi=false) or high (hi=true) half of `old`.
+template <bool HI>
+__device__ inline int cvt_pk_fp8(float a, float b, int old) {
+  return __builtin_amdgcn_cvt_pk_fp8_f32(a, b, old, HI);
+}
+// Four floats -> four e4m3fn bytes in one dword (byte i = element i).
+__device__ inline int cvt_fp8x4(float a, float b, float c, float d) {
+  int v = cvt_pk_fp8<false>(a, b, 0);
+  return cvt_pk_fp8<true>(c, d, v);
+}
+__device__ inline float clamp_fp8(float x) { return fminf(fmaxf(x, -kFp8Max), kFp8Max); }
+
+// ------------------------------------------------------------ wave helpers
+__device__ inline int lane_id() { return __lane_id(); }
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Max over aligned groups of `W` lanes (W a power of two <= 64).
+template <int W>
+__device__ inline float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ inline int wave_incl_scan(int v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int t = __shfl_up(v, o, 64);
+    if (l >= o) v += t;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------- MFMA
+// 16x16x128 FP8 (e4m3fn x e4m3fn), fp32 accumulate.  Operand layout (both A
+// and B): lane l supplies row/column (l % 16) and 32 consecutive K bytes at
+// K offset (l / 16) * 32.  Result: lane l holds C[4*(l/16) + r][l % 16].
+__device__ inline v4f mfma_fp8_16x16x128(v8i a, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+// 16x16x32 bf16 / fp16: lane l supplies row (l % 16) and 8 consecutive K
+// elements at K offset (l / 16) * 8.  Same C layout as above.
+__device__ inline v4f mfma_bf16_16x16x32(v8s a, v8s b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a),
+                                                 __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+}
+__device__ inline v4f mfma_f16_16x16x32(v8s a, v8s b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a),
+                                                __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+template <int DT>
+__device__ inline v4f mfma_h16(v8s a, v8s b, v4f c) {
+  if constexpr (DT == kBF16) return mfma_bf16_16x16x32(a, b, c);
+  else return mfma_f16_16x16x32(a, b, c);
+}
+
+__device__ inline float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
+__device__ inline float gelu_tanh_f32(float x) {
+  const float k = 0.7978845608028654f;
+  float t = k * (x + 0.044715f * x * x * x);
+  float th = 2.0f / (1.0f + __expf(-2.0f * t)) - 1.0f;
+  return 0.5f * x * (1.0f + th);
+}
+template <int ACT>
+__device__ inline float act_f32(float x) {
+  if constexpr (ACT == 0) return silu_f32(x);
+  else return gelu_tanh_f32(x);
+}
+
+}  // namespace mstar

@@ -1,0 +1,79 @@
+// Host-side launchers shared between the kernel translation units and the
+// C-ABI layer.  Every launcher validates its arguments, enqueues on the
+// stream it is given and returns a Status code; nothing allocates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mstar {
+
+// route.hip
+int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, int k,
+                        int renorm, float* w, int32_t* ids32, int64_t* ids64, hipStream_t stream);
+int launch_align(const void* ids, int ids_dtype, int64_t numel, int E, int bm,
+                 int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, int64_t max_padded,
+                 int32_t* expert_off, int32_t* expert_cnt, hipStream_t stream);
+
+// quant.hip
+int launch_quant_fp8_group(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                           int64_t ld_x, uint8_t* q, float* s, hipStream_t stream);
+int launch_quant_fp8_row(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q,
+                         float* s, hipStream_t stream);
+
+// elementwise.hip
+int launch_act_and_mul(const void* gate_up, void* out, int dtype, int64_t rows, int64_t inter,
+                       int activation, hipStream_t stream);
+int launch_sum_reduce(const void* in, void* out, int dtype, int64_t tokens, int64_t topk,
+                      int64_t hidden, float scale, hipStream_t stream);
+
+// moe_gemm.hip --------------------------------------------------------------
+// Operand encodings.
+enum AKind : int { A_H16 = 0, A_FP8G = 1, A_FP8R = 2 };
+enum BKind : int { B_H16 = 0, B_FP8BLK = 1, B_INT4G = 2, B_FP8R = 3 };
+enum EpiKind : int { EPI_STORE = 0, EPI_ACT = 1, EPI_DENSE = 2 };
+
+struct GemmArgs {
+  // A: activations, rows of K elements (bytes for fp8), row stride lda.
+  const void* A;
+  int64_t lda;
+  const float* a_scale;  // A_FP8G: [rows, K/128] (stride ld_as); A_FP8R: [rows]
+  int64_t ld_as;
+  // B: weights [E][N][K] (B_INT4G: [E][N][K/8] int32 words).
+  const void* B;
+  int64_t ldb;        // row stride in elements (int4: int32 words)
+  int64_t b_estride;  // expert stride in elements (int4: words)
+  const void* b_scale;  // B_FP8BLK: fp32 [E][ceil(N/128)][K/128]; B_INT4G: 16-bit [E][N][K/128];
+                        // B_FP8R: fp32 [N]
+  int64_t bs_estride;
+  int64_t bs_ld;
+  void* C;
+  int64_t ldc;
+  const void* topk_w;  // per slot routing weight (EPI_STORE with mul_routed)
+  int topk_w_dtype;
+  const int32_t* sorted_ids;  // grouped mode
+  const int32_t* expert_ids;
+  const int32_t* ntpp;
+  const int32_t* expert_off;  // streaming mode: [E+1] padded starts
+  const int32_t* expert_cnt;  // streaming mode: [E] real counts
+  int64_t M;          // dense: rows; grouped: number of valid slots (numel)
+  int N, K;
+  int top_k;          // A row = slot / top_k
+  int inter;          // EPI_ACT: gate/up split (N == 2 * inter)
+  int mul_routed;
+  int activation;     // 0 silu, 1 gelu
+  int num_experts;
+  int m_blocks;       // grouped: number of m-blocks (expert_ids length)
+};
+
+// Tiled grouped / dense GEMM (LDS-staged MFMA tiles); bm is the row block.
+int launch_tile_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dtype, bool grouped,
+                     int bm, hipStream_t stream);
+// Weight-streaming grouped GEMM for small token counts (one workgroup per
+// (expert, n-tile); each weight byte is read once).  A_H16 with B_FP8BLK
+// quantises the activations per 128-group on the fly.
+int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dtype,
+                       int max_rows, hipStream_t stream);
+bool stream_gemm_supported(int K, int max_rows, int akind, int bkind);
+
+}  // namespace mstar

@@ -1,0 +1,119 @@
+"""MoE blocks and the router (drop-in for mstar/model/components/moe.py).
+
+* :class:`TopKRouter` -- ``F.linear`` gate projection, then the HIP
+  softmax-top-k kernel (moe.py:85-140); returns ``(weights fp32, ids int64,
+  None)`` like the reference's 3-tuple router contract.
+* :func:`dispatch` -- the fused path (moe.py:188-205 minus the naive
+  fallback: these kernels are the only compute path; CPU tensors raise).
+* :class:`SparseMoeBlock` / :class:`SparseMoeBlockWithSharedExpert` --
+  the reference blocks (moe.py:208-328) with the same parameter layout
+  (``experts.gate_up_proj [E, 2I, H]`` rows ``[gate; up]``,
+  ``experts.down_proj [E, H, I]``) plus :meth:`quantize` to switch the
+  experts to FP8 (block 128x128) or W4A16 (group 128) storage.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops, quant
+from .fused_moe import fused_experts
+
+
+class TopKRouter(nn.Module):
+    def __init__(self, hidden_size: int, num_experts: int, num_experts_per_tok: int,
+                 norm_topk_prob: bool = True) -> None:
+        super().__init__()
+        self.top_k = num_experts_per_tok
+        self.num_experts = num_experts
+        self.norm_topk_prob = norm_topk_prob
+        self.weight = nn.Parameter(torch.zeros(num_experts, hidden_size))
+
+    def forward(self, hidden_states: torch.Tensor, router_states: torch.Tensor | None = None):
+        hidden_states = hidden_states.reshape(-1, hidden_states.shape[-1])
+        router_logits = F.linear(hidden_states, self.weight)
+        w, ids = ops.topk_softmax(router_logits, self.top_k, self.norm_topk_prob)
+        return w, ids, None
+
+
+class _Experts(nn.Module):
+    def __init__(self, num_experts: int, hidden_size: int, inter: int) -> None:
+        super().__init__()
+        self.gate_up_proj = nn.Parameter(torch.empty(num_experts, 2 * inter, hidden_size))
+        self.down_proj = nn.Parameter(torch.empty(num_experts, hidden_size, inter))
+        self.quant: str | None = None
+        self.register_buffer("w1_scale", None)
+        self.register_buffer("w2_scale", None)
+
+    @torch.no_grad()
+    def quantize(self, mode: str) -> None:
+        """Replace the bf16 expert weights by ``mode`` storage in place."""
+        if self.quant is not None:
+            raise RuntimeError(f"experts already quantised ({self.quant})")
+        w1, w2 = self.gate_up_proj.data, self.down_proj.data
+        if mode == "fp8_w8a8":
+            q1, s1 = quant.quantize_fp8_block(w1)
+            q2, s2 = quant.quantize_fp8_block(w2)
+        elif mode == "w4a16":
+            q1, s1 = quant.quantize_int4_group(w1)
+            q2, s2 = quant.quantize_int4_group(w2)
+        else:
+            raise ValueError(f"unknown quantisation mode {mode!r}")
+        self.gate_up_proj = nn.Parameter(q1, requires_grad=False)
+        self.down_proj = nn.Parameter(q2, requires_grad=False)
+        self.w1_scale = s1
+        self.w2_scale = s2
+        self.quant = mode
+
+
+def dispatch(hidden_states, experts: _Experts, num_experts, selected_experts, routing_weights):
+    return fused_experts(hidden_states, experts.gate_up_proj, experts.down_proj, routing_weights,
+                         selected_experts, quant=experts.quant, w1_scale=experts.w1_scale,
+                         w2_scale=experts.w2_scale)
+
+
+class SparseMoeBlock(nn.Module):
+    def __init__(self, hidden_size: int, num_experts: int, num_experts_per_tok: int,
+                 moe_intermediate_size: int, norm_topk_prob: bool = True,
+                 router: nn.Module | None = None) -> None:
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.num_experts = num_experts
+        self.num_experts_per_tok = num_experts_per_tok
+        self.moe_intermediate_size = moe_intermediate_size
+        self.gate = router if router is not None else TopKRouter(
+            hidden_size, num_experts, num_experts_per_tok, norm_topk_prob)
+        self.experts = _Experts(num_experts, hidden_size, moe_intermediate_size)
+
+    def quantize(self, mode: str) -> "SparseMoeBlock":
+        self.experts.quantize(mode)
+        return self
+
+    def forward(self, hidden_states, router_states=None, *, return_router_states: bool = False):
+        input_shape = hidden_states.shape
+        flat = hidden_states.view(-1, hidden_states.shape[-1]).contiguous()
+        w, ids, router_states_next = self.gate(flat, router_states)
+        out = dispatch(flat, self.experts, self.num_experts, ids, w).view(input_shape)
+        return (out, router_states_next) if return_router_states else out
+
+
+class SparseMoeBlockWithSharedExpert(SparseMoeBlock):
+    """``out = routed(x) + sigmoid(shared_gate(x)) * shared_expert(x)`` (moe.py:264-328)."""
+
+    def __init__(self, hidden_size: int, num_experts: int, num_experts_per_tok: int,
+                 moe_intermediate_size: int, shared_expert: nn.Module,
+                 norm_topk_prob: bool = False, router: nn.Module | None = None) -> None:
+        super().__init__(hidden_size, num_experts, num_experts_per_tok, moe_intermediate_size,
+                         norm_topk_prob, router)
+        self.shared_expert = shared_expert
+        self.shared_expert_gate = nn.Linear(hidden_size, 1, bias=False)
+
+    def forward(self, hidden_states, router_states=None, *, return_router_states: bool = False):
+        input_shape = hidden_states.shape
+        flat = hidden_states.view(-1, hidden_states.shape[-1]).contiguous()
+        shared = self.shared_expert(flat)
+        w, ids, router_states_next = self.gate(flat, router_states)
+        routed = dispatch(flat, self.experts, self.num_experts, ids, w)
+        out = (routed + torch.sigmoid(self.shared_expert_gate(flat)) * shared).view(input_shape)
+        return (out, router_states_next) if return_router_states else out
