@@ -102,6 +102,31 @@ int mstar_moe_grouped_gemm(const void* A, const void* B, void* C, const void* to
                            int64_t N, int64_t K, int64_t em, int64_t num_valid_tokens, int top_k,
                            int mul_routed_weight, int block_size, int dtype, void* stream);
 
+/* Grouped GEMM with the quantised variants and the fused activation -- one
+ * stage of mstar_fused_moe, exposed for callers that run the stages
+ * themselves (e.g. tensor-parallel shards).  Replaces invoke_fused_moe_kernel
+ * (mstar/utils/fused_moe/kernels.py:141-218) and the fp8_w8a8 / int4_w4a16
+ * branches the reference stripped from it (kernels.py:3-7).
+ *   A: [rows, K] bf16/fp16, or e4m3fn with a_scale [rows, K/128] (tiled path);
+ *   B: quant NONE [E, N, K] 16-bit; FP8_W8A8 [E, N, K] e4m3fn + b_scale fp32
+ *      [E, ceil(N/128), K/128]; W4A16 [E, N, K/8] int32 + b_scale bf16
+ *      [E, N, K/128];
+ *   activation = -1: C[slot, :N] = dt(acc (* topk_weights[slot]));
+ *   activation = 0 (silu) / 1 (gelu): B rows are [gate; up] (N = 2I) and
+ *      C[slot, :I] = dt(dt(act(dt(gate))) * dt(up)) (the act_and_mul fused).
+ *   path: 0 = auto, 1 = LDS-tiled (needs expert_ids/num_tokens_post_padded
+ *   from mstar_moe_align_block_size with this block_size), 2 = weight
+ *   streaming (needs expert_offsets/expert_counts; 16-bit A, quantised B;
+ *   FP8 activations are quantised per 128-group on the fly).
+ * The A row of a slot is slot / top_k. */
+int mstar_moe_gemm(const void* A, int a_dtype, const float* a_scale, const void* B, int quant,
+                   const void* b_scale, void* C, int c_dtype, const void* topk_weights,
+                   int topk_w_dtype, const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                   const int32_t* num_tokens_post_padded, const int32_t* expert_offsets,
+                   const int32_t* expert_counts, int num_experts, int64_t N, int64_t K,
+                   int64_t em, int64_t num_valid_tokens, int top_k, int mul_routed_weight,
+                   int activation, int block_size, int path, void* stream);
+
 /* Workspace bytes mstar_fused_moe needs for these sizes. */
 int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
                                    int64_t inter, int top_k, int quant, int act_dtype,

@@ -203,6 +203,71 @@ int mstar_moe_grouped_gemm(const void* A, const void* B, void* C, const void* to
                           (hipStream_t)stream);
 }
 
+int mstar_moe_gemm(const void* A, int a_dtype, const float* a_scale, const void* B, int quant,
+                   const void* b_scale, void* C, int c_dtype, const void* topk_weights,
+                   int topk_w_dtype, const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                   const int32_t* num_tokens_post_padded, const int32_t* expert_offsets,
+                   const int32_t* expert_counts, int num_experts, int64_t N, int64_t K,
+                   int64_t em, int64_t num_valid_tokens, int top_k, int mul_routed_weight,
+                   int activation, int block_size, int path, void* stream) {
+  if (N <= 0 || K <= 0 || K % 128 != 0 || num_experts <= 0 || top_k <= 0 || !A || !B || !C ||
+      !sorted_token_ids || (mul_routed_weight && !topk_weights) ||
+      (quant != MSTAR_QUANT_NONE && !b_scale) || activation < -1 || activation > 1 ||
+      (activation >= 0 && N % 2 != 0) || path < 0 || path > 2) {
+    set_last_error("moe_gemm: invalid arguments (N=%lld K=%lld quant=%d act=%d path=%d)",
+                   (long long)N, (long long)K, quant, activation, path);
+    return kInvalidArgument;
+  }
+  const int bkind = quant == MSTAR_QUANT_FP8_W8A8 ? B_FP8BLK : quant == MSTAR_QUANT_W4A16 ? B_INT4G : B_H16;
+  GemmArgs g = {};
+  g.A = A; g.lda = K; g.a_scale = a_scale; g.ld_as = K / 128;
+  g.B = B; g.b_scale = b_scale;
+  if (bkind == B_FP8BLK) {
+    g.ldb = K; g.b_estride = N * K; g.bs_ld = K / 128; g.bs_estride = ((N + 127) / 128) * (K / 128);
+  } else if (bkind == B_INT4G) {
+    g.ldb = K / 8; g.b_estride = N * (K / 8); g.bs_ld = K / 128; g.bs_estride = N * (K / 128);
+  } else {
+    g.ldb = K; g.b_estride = N * K;
+  }
+  g.C = C; g.ldc = activation >= 0 ? N / 2 : N;
+  g.topk_w = topk_weights; g.topk_w_dtype = topk_w_dtype;
+  g.sorted_ids = sorted_token_ids; g.expert_ids = expert_ids; g.ntpp = num_tokens_post_padded;
+  g.expert_off = expert_offsets; g.expert_cnt = expert_counts;
+  g.M = num_valid_tokens; g.N = (int)N; g.K = (int)K; g.top_k = top_k;
+  g.inter = (int)(N / 2); g.mul_routed = mul_routed_weight;
+  g.activation = activation < 0 ? 0 : activation; g.num_experts = num_experts;
+  g.m_blocks = block_size > 0 ? (int)((em + block_size - 1) / block_size) : 0;
+  const int epi = activation >= 0 ? EPI_ACT : EPI_STORE;
+  const bool a16 = a_dtype == kBF16 || a_dtype == kF16;
+  if (path == 2 || (path == 0 && a16 && bkind != B_H16 && expert_offsets && expert_counts &&
+                    stream_gemm_supported((int)K, 0, A_H16, bkind) &&
+                    num_valid_tokens <= 64 * top_k)) {
+    if (!a16) {
+      set_last_error("moe_gemm: the streaming path takes 16-bit activations");
+      return kUnsupported;
+    }
+    return launch_stream_gemm(g, A_H16, bkind, epi, a_dtype, 0, (hipStream_t)stream);
+  }
+  if (!expert_ids || !num_tokens_post_padded) {
+    set_last_error("moe_gemm: the tiled path needs expert_ids and num_tokens_post_padded");
+    return kInvalidArgument;
+  }
+  int akind = A_H16;
+  if (a_dtype == kFP8) {
+    if (!a_scale) {
+      set_last_error("moe_gemm: FP8 activations need per-128-group scales");
+      return kInvalidArgument;
+    }
+    akind = A_FP8G;
+  }
+  if ((akind == A_FP8G) != (bkind == B_FP8BLK)) {
+    set_last_error("moe_gemm: FP8 weights need FP8 activations on the tiled path");
+    return kUnsupported;
+  }
+  const int dt = a16 ? a_dtype : c_dtype;
+  return launch_tile_gemm(g, akind, bkind, epi, dt, true, block_size, (hipStream_t)stream);
+}
+
 int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
                                    int64_t inter, int top_k, int quant, int act_dtype,
                                    int reduce_results, size_t* bytes) {

@@ -137,6 +137,13 @@ __device__ inline v4f mfma_h16(v8s a, v8s b, v4f c) {
   else return mfma_f16_16x16x32(a, b, c);
 }
 
+// One routing weight, stored as fp32, bf16 or fp16.
+__device__ inline float load_weight_any(const void* w, int dtype, int64_t i) {
+  if (dtype == kF32) return ((const float*)w)[i];
+  const uint16_t b = ((const uint16_t*)w)[i];
+  return dtype == kBF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
 __device__ inline float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
 __device__ inline float gelu_tanh_f32(float x) {
   const float k = 0.7978845608028654f;

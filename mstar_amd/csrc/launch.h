@@ -76,4 +76,9 @@ int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dty
                        int max_rows, hipStream_t stream);
 bool stream_gemm_supported(int K, int max_rows, int akind, int bkind);
 
+// stream_fp8.hip: persistent FP8 weight streaming (bf16 activations,
+// quantised per 128-group on the fly).
+int launch_stream_fp8(const GemmArgs& a, int epi, hipStream_t stream);
+bool stream_fp8_supported(int K, int N, int inter, int epi);
+
 }  // namespace mstar

@@ -33,9 +33,7 @@ namespace mstar {
 // Shared helpers
 // ---------------------------------------------------------------------------
 __device__ inline float load_weight(const void* w, int dtype, int64_t i) {
-  if (dtype == kF32) return ((const float*)w)[i];
-  const uint16_t b = ((const uint16_t*)w)[i];
-  return dtype == kBF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+  return load_weight_any(w, dtype, i);
 }
 
 // 32 bytes from a 16-byte aligned address (LDS rows are padded to 16 bytes,
@@ -624,9 +622,7 @@ int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dty
     set_last_error("stream_gemm: missing expert offsets/counts or bad shapes");
     return kInvalidArgument;
   }
-  if (bkind == B_FP8BLK)
-    return epi == EPI_ACT ? dispatch_ks<B_FP8BLK, EPI_ACT>(a, stream)
-                          : dispatch_ks<B_FP8BLK, EPI_STORE>(a, stream);
+  if (bkind == B_FP8BLK) return launch_stream_fp8(a, epi, stream);
   return epi == EPI_ACT ? dispatch_ks<B_INT4G, EPI_ACT>(a, stream)
                         : dispatch_ks<B_INT4G, EPI_STORE>(a, stream);
 }

@@ -300,16 +300,16 @@ int launch_align(const void* ids, int ids_dtype, int64_t numel, int E, int bm,
     return kUnsupported;
   }
   size_t shmem = sizeof(int) * ((size_t)kAlignWaves * E + (E + 1) + E + kAlignWaves);
-  static bool attr_set = false;  // LDS beyond 64 KB needs an explicit opt-in
-  if (!attr_set) {
+  static size_t attr_bytes = 0;  // LDS beyond 64 KB needs an explicit opt-in
+  if (shmem > 64 * 1024 && shmem > attr_bytes) {
     if (hipFuncSetAttribute((const void*)align_kernel<int32_t>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess ||
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem) != hipSuccess ||
         hipFuncSetAttribute((const void*)align_kernel<int64_t>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
-      set_last_error("moe_align_block_size: cannot reserve LDS");
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem) != hipSuccess) {
+      set_last_error("moe_align_block_size: cannot reserve %zu bytes of LDS", shmem);
       return kLaunchError;
     }
-    attr_set = true;
+    attr_bytes = shmem;
   }
   if (ids_dtype == kI32)
     align_kernel<int32_t><<<1, kAlignThreads, shmem, stream>>>(

@@ -257,3 +257,36 @@ def test_block_quantize_fp8():
     # FP8 weights and activations: within a few percent of the bf16 block.
     err = (out.float() - ref.float()).abs().max() / ref.float().abs().max()
     assert float(err) < 0.1
+
+
+# ----------------------------------------------------------- graph capture
+def test_layer_under_hip_graph_replays():
+    """Route + fused FP8 layer captured in a HIP graph: every replay (with
+    eager work and syncs in between) equals the eager result bit for bit."""
+    from mstar_amd import ops
+    from mstar_amd.fused_moe import fused_experts
+    H, E, I, k = 2048, 128, 768, 8
+    q1, s1, q2, s2 = _fp8_weights(H, E, I)
+    for M in (32, 300):
+        x = _hidden(M, H, seed=11).to(DEV)
+        logits = torch.randn(M, E, device=DEV)
+
+        def fn():
+            w, ids = ops.topk_softmax(logits, k, True)
+            return fused_experts(x, q1, q2, w, ids, quant="fp8_w8a8", w1_scale=s1, w2_scale=s2)
+
+        eager = fn()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = fn()
+        for _ in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
+            _ = fn()  # eager work between replays
+            torch.cuda.synchronize()
