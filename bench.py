@@ -86,11 +86,12 @@ def make_inputs(M, bias, seed=0):
 
 
 def layer(x, logits, w):
-    from mstar_amd import ops
-    from mstar_amd.fused_moe import fused_experts
+    """Routing from logits + the routed experts: one library call
+    (mstar_moe_layer), as SparseMoeBlock runs it after the gate projection."""
+    from mstar_amd import _lib, ops
     q1, s1, q2, s2 = w
-    tw, ti = ops.topk_softmax(logits, K_TOP, True)
-    return fused_experts(x, q1, q2, tw, ti, quant="fp8_w8a8", w1_scale=s1, w2_scale=s2)
+    out, _, _ = ops.moe_layer(x, logits, q1, q2, K_TOP, True, 0, _lib.QUANT_FP8_W8A8, s1, s2)
+    return out
 
 
 def capture(fn):
@@ -146,7 +147,7 @@ def gate_up_kernel_timing(x, logits, weights, steps, warmup):
     _lib.check(lib.mstar_moe_align_block_size(ti.data_ptr(), _lib.DT_I64, slots, E, bm,
                                               sorted_ids.data_ptr(), max_padded, eids.data_ptr(),
                                               max_blocks, ntpp.data_ptr(), eoff.data_ptr(),
-                                              ecnt.data_ptr(), sp), "align")
+                                              ecnt.data_ptr(), None, 0, sp), "align")
     c2 = torch.empty(slots, INTER, dtype=torch.bfloat16, device=dev)
 
     def launch(w):

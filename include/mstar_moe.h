@@ -76,7 +76,30 @@ int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t nume
                                int num_experts, int block_size, int32_t* sorted_token_ids,
                                int64_t sorted_len, int32_t* expert_ids, int64_t expert_ids_len,
                                int32_t* num_tokens_post_pad, int32_t* expert_offsets,
-                               int32_t* expert_counts, void* stream);
+                               int32_t* expert_counts, void* scratch, size_t scratch_bytes,
+                               void* stream);
+
+/* Scratch for mstar_moe_align_block_size's grid-wide path (numel > 4096).
+ * With scratch NULL the alignment runs in one workgroup (same result,
+ * slower for large numel).  The reference allocates its own cumsum buffer
+ * inside the op (moe_align_block_size.cu:230); here the caller passes it. */
+int mstar_moe_align_scratch_size(int64_t numel, int num_experts, size_t* bytes);
+
+/* Softmax top-k + alignment in one call: mstar_moe_topk_softmax followed by
+ * mstar_moe_align_block_size on its ids (one launch when
+ * num_tokens*top_k <= 4096, else two).  Replaces the router's
+ * softmax/topk/renormalise (mstar/model/components/moe.py:131-139) plus
+ * moe_align_block_size (mstar/utils/fused_moe/align.py:55-103) as the
+ * reference runs them back to back.  topk_ids_i32 and topk_ids_i64 may be
+ * NULL (the int32 ids then live in scratch).  scratch: see
+ * mstar_moe_route_scratch_size (required above 4096 slots). */
+int mstar_moe_route(const void* router_logits, int logits_dtype, int64_t num_tokens,
+                    int num_experts, int top_k, int renormalize, float* topk_weights,
+                    int32_t* topk_ids_i32, int64_t* topk_ids_i64, int block_size,
+                    int32_t* sorted_token_ids, int64_t sorted_len, int32_t* expert_ids,
+                    int64_t expert_ids_len, int32_t* num_tokens_post_pad, int32_t* expert_offsets,
+                    int32_t* expert_counts, void* scratch, size_t scratch_bytes, void* stream);
+int mstar_moe_route_scratch_size(int64_t num_tokens, int num_experts, int top_k, size_t* bytes);
 
 /* out[r, :] = dt(dt(act_f32(gate_up[r, :I])) * gate_up[r, I:]).
  * Replaces act_and_mul_triton (mstar/utils/fused_moe/kernels.py:279-298).
@@ -153,6 +176,27 @@ int mstar_fused_moe(const void* hidden, int act_dtype, int64_t num_tokens, int64
                     const void* w1_scale, const void* w2_scale, const void* topk_weights,
                     int topk_w_dtype, const void* topk_ids, int ids_dtype, int top_k,
                     int activation, int reduce_results, void* out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* Workspace bytes mstar_moe_layer needs for these sizes. */
+int mstar_moe_layer_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
+                                   int64_t inter, int top_k, int quant, int act_dtype,
+                                   size_t* bytes);
+
+/* A routed MoE layer from the router logits: softmax top-k (+ renormalise)
+ * -> align -> gate_up GEMM (+ activation) -> down GEMM (x routed weight) ->
+ * top-k sum into out [num_tokens, hidden_size].  Replaces the routed half of
+ * SparseMoeBlock.forward after the gate projection
+ * (mstar/model/components/moe.py:245-261: TopKRouter from its logits on,
+ * then _dispatch -> fused_experts).  Same weight formats as
+ * mstar_fused_moe.  topk_weights_out [num_tokens, top_k] fp32 and
+ * topk_ids_out [num_tokens, top_k] int64 are optional copies of the routing
+ * (the reference router returns them). */
+int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                    const void* router_logits, int logits_dtype, int renormalize, const void* w1,
+                    const void* w2, int num_experts, int64_t inter, int quant,
+                    const void* w1_scale, const void* w2_scale, int top_k, int activation,
+                    void* out, float* topk_weights_out, int64_t* topk_ids_out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
 /* Activation quantisation, OCP e4m3fn: per token-group of 128

@@ -38,7 +38,13 @@ SIGNATURES = {
     "mstar_moe_abi_version": (_c_int, []),
     "mstar_moe_topk_softmax": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
     "mstar_moe_align_block_size": (
-        _c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _vp]),
+        _c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _vp,
+                 ctypes.c_size_t, _vp]),
+    "mstar_moe_align_scratch_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(ctypes.c_size_t)]),
+    "mstar_moe_route": (
+        _c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_i64,
+                 _vp, _c_i64, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "mstar_moe_route_scratch_size": (_c_int, [_c_i64, _c_int, _c_int, ctypes.POINTER(ctypes.c_size_t)]),
     "mstar_moe_act_and_mul": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_int, _vp]),
     "mstar_moe_sum_reduce": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _f32, _vp]),
     "mstar_moe_grouped_gemm": (
@@ -54,6 +60,12 @@ SIGNATURES = {
     "mstar_fused_moe": (
         _c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _vp, _c_int, _c_i64, _c_int, _vp, _vp, _vp,
                  _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, ctypes.c_size_t, _vp]),
+    "mstar_moe_layer_workspace_size": (
+        _c_int, [_c_i64, _c_i64, _c_int, _c_i64, _c_int, _c_int, _c_int,
+                 ctypes.POINTER(ctypes.c_size_t)]),
+    "mstar_moe_layer": (
+        _c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _c_int, _vp, _vp, _c_int, _c_i64, _c_int,
+                 _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "mstar_quant_fp8_per_token_group": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _vp, _vp, _vp]),
     "mstar_quant_fp8_per_token": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mstar_fp8_scaled_mm": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),

@@ -53,11 +53,13 @@ struct Plan {
   int bm = 16;
   int64_t slots = 0, max_padded = 0, max_blocks = 0;
   size_t off_sorted, off_eids, off_ntpp, off_eoff, off_ecnt, off_c2, off_c3, off_hq, off_hs,
-      off_cq, off_cs, total;
+      off_cq, off_cs, off_scratch, scratch_bytes, off_tw, off_ids, total;
 };
 
+// with_route: the plan also holds the router outputs and the routing scratch
+// (mstar_moe_layer); otherwise only the alignment scratch (mstar_fused_moe).
 static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quant, int act_dtype,
-                     int reduce, Plan* pl) {
+                     int reduce, Plan* pl, bool with_route = false) {
   if (M < 0 || H <= 0 || E <= 0 || I <= 0 || top_k <= 0 || top_k > E) {
     set_last_error("fused_moe: invalid sizes (M=%lld H=%lld E=%d I=%lld top_k=%d)",
                    (long long)M, (long long)H, E, (long long)I, top_k);
@@ -98,7 +100,106 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->off_hs = fp8_tiled ? take((size_t)M * (H / 128) * 4) : 0;
   pl->off_cq = fp8_tiled ? take((size_t)pl->slots * I) : 0;
   pl->off_cs = fp8_tiled ? take((size_t)pl->slots * (I / 128) * 4) : 0;
+  pl->scratch_bytes = with_route ? route_scratch_bytes(M, top_k, E) : align_scratch_bytes(pl->slots, E);
+  pl->off_scratch = take(pl->scratch_bytes);
+  pl->off_tw = with_route ? take((size_t)pl->slots * 4) : 0;
+  pl->off_ids = with_route ? take((size_t)pl->slots * 4) : 0;
   pl->total = o;
+  return kOk;
+}
+
+
+static int check_layer_args(const Plan& pl, int activation, void* workspace, size_t workspace_bytes) {
+  if (activation != 0 && activation != 1) {
+    set_last_error("fused_moe: activation must be 0 (silu) or 1 (gelu)");
+    return kInvalidArgument;
+  }
+  if (workspace_bytes < pl.total || (pl.total > 0 && !workspace)) {
+    set_last_error("fused_moe: workspace too small (%zu < %zu)", workspace_bytes, pl.total);
+    return kWorkspaceTooSmall;
+  }
+  return kOk;
+}
+
+// Everything after the alignment: gate_up GEMM (+ activation), down GEMM
+// (x routed weight), top-k sum.  The alignment outputs are in `ws`.
+static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_t num_tokens,
+                       int64_t hidden_size, const void* w1, const void* w2, int num_experts,
+                       int64_t inter, int quant, const void* w1_scale, const void* w2_scale,
+                       const void* topk_weights, int topk_w_dtype, int top_k, int activation,
+                       int reduce_results, void* out, uint8_t* ws, hipStream_t stream) {
+  const int64_t M = num_tokens, H = hidden_size, I = inter;
+  const int E = num_experts;
+  int st = kOk;
+  int32_t* sorted = (int32_t*)(ws + pl.off_sorted);
+  int32_t* eids = (int32_t*)(ws + pl.off_eids);
+  int32_t* ntpp = (int32_t*)(ws + pl.off_ntpp);
+  int32_t* eoff = (int32_t*)(ws + pl.off_eoff);
+  int32_t* ecnt = (int32_t*)(ws + pl.off_ecnt);
+  void* cache2 = ws + pl.off_c2;
+  void* cache3 = reduce_results ? (void*)(ws + pl.off_c3) : out;
+  const int bkind = quant == MSTAR_QUANT_FP8_W8A8 ? B_FP8BLK : quant == MSTAR_QUANT_W4A16 ? B_INT4G : B_H16;
+  GemmArgs g1 = {};
+  g1.B = w1;
+  g1.C = cache2; g1.ldc = I;
+  g1.sorted_ids = sorted; g1.expert_ids = eids; g1.ntpp = ntpp;
+  g1.expert_off = eoff; g1.expert_cnt = ecnt;
+  g1.M = pl.slots; g1.N = (int)(2 * I); g1.K = (int)H; g1.top_k = top_k; g1.inter = (int)I;
+  g1.activation = activation; g1.num_experts = E; g1.m_blocks = (int)pl.max_blocks;
+  g1.topk_w = topk_weights; g1.topk_w_dtype = topk_w_dtype;
+  GemmArgs g2 = g1;
+  g2.B = w2;
+  g2.C = cache3; g2.ldc = H;
+  g2.N = (int)H; g2.K = (int)I; g2.top_k = 1; g2.mul_routed = 1;
+  g2.A = cache2; g2.lda = I;
+
+  if (bkind == B_FP8BLK) {
+    // w1: [E][2I][H] e4m3fn, scales [E][2I/128][H/128]; w2: [E][H][I], [E][H/128][I/128].
+    g1.ldb = H; g1.b_estride = 2 * I * H; g1.b_scale = w1_scale;
+    g1.bs_ld = H / 128; g1.bs_estride = (2 * I / 128) * (H / 128);
+    g2.ldb = I; g2.b_estride = H * I; g2.b_scale = w2_scale;
+    g2.bs_ld = I / 128; g2.bs_estride = (H / 128) * (I / 128);
+  } else if (bkind == B_INT4G) {
+    // w1: [E][2I][H/8] int32, scales [E][2I][H/128] bf16; w2: [E][H][I/8], [E][H][I/128].
+    g1.ldb = H / 8; g1.b_estride = 2 * I * (H / 8); g1.b_scale = w1_scale;
+    g1.bs_ld = H / 128; g1.bs_estride = 2 * I * (H / 128);
+    g2.ldb = I / 8; g2.b_estride = H * (I / 8); g2.b_scale = w2_scale;
+    g2.bs_ld = I / 128; g2.bs_estride = H * (I / 128);
+  } else {
+    g1.ldb = H; g1.b_estride = 2 * I * H;
+    g2.ldb = I; g2.b_estride = H * I;
+  }
+
+  if (pl.stream) {
+    g1.A = hidden; g1.lda = H;
+    st = launch_stream_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, (int)M, stream);
+    if (st != kOk) return st;
+    st = launch_stream_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, (int)M, stream);
+    if (st != kOk) return st;
+  } else if (bkind == B_FP8BLK) {
+    uint8_t* hq = ws + pl.off_hq;
+    float* hs = (float*)(ws + pl.off_hs);
+    uint8_t* cq = ws + pl.off_cq;
+    float* cs = (float*)(ws + pl.off_cs);
+    st = launch_quant_fp8_group(hidden, act_dtype, M, H, H, hq, hs, stream);
+    if (st != kOk) return st;
+    g1.A = hq; g1.lda = H; g1.a_scale = hs; g1.ld_as = H / 128;
+    st = launch_tile_gemm(g1, A_FP8G, B_FP8BLK, EPI_ACT, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+    st = launch_quant_fp8_group(cache2, act_dtype, pl.slots, I, I, cq, cs, stream);
+    if (st != kOk) return st;
+    g2.A = cq; g2.lda = I; g2.a_scale = cs; g2.ld_as = I / 128;
+    st = launch_tile_gemm(g2, A_FP8G, B_FP8BLK, EPI_STORE, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+  } else {
+    g1.A = hidden; g1.lda = H;
+    st = launch_tile_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+    st = launch_tile_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+  }
+  if (reduce_results)
+    return launch_sum_reduce(cache3, out, act_dtype, M, top_k, H, 1.0f, stream);
   return kOk;
 }
 
@@ -123,7 +224,8 @@ int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t nume
                                int num_experts, int block_size, int32_t* sorted_token_ids,
                                int64_t sorted_len, int32_t* expert_ids, int64_t expert_ids_len,
                                int32_t* num_tokens_post_pad, int32_t* expert_offsets,
-                               int32_t* expert_counts, void* stream) {
+                               int32_t* expert_counts, void* scratch, size_t scratch_bytes,
+                               void* stream) {
   if (block_size > 0 && expert_ids_len < (sorted_len + block_size - 1) / block_size) {
     set_last_error("moe_align_block_size: experts_ids too small (%lld < %lld)",
                    (long long)expert_ids_len,
@@ -132,7 +234,7 @@ int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t nume
   }
   return launch_align(topk_ids, ids_dtype, numel, num_experts, block_size, sorted_token_ids,
                       expert_ids, num_tokens_post_pad, sorted_len, expert_offsets, expert_counts,
-                      (hipStream_t)stream);
+                      scratch, scratch_bytes, (hipStream_t)stream);
 }
 
 int mstar_moe_act_and_mul(const void* gate_up, void* out, int dtype, int64_t rows, int64_t inter,
@@ -289,97 +391,95 @@ int mstar_fused_moe(const void* hidden, int act_dtype, int64_t num_tokens, int64
   int st = make_plan(num_tokens, hidden_size, num_experts, inter, top_k, quant, act_dtype,
                      reduce_results, &pl);
   if (st != kOk) return st;
-  if (activation != 0 && activation != 1) {
-    set_last_error("fused_moe: activation must be 0 (silu) or 1 (gelu)");
-    return kInvalidArgument;
-  }
-  if (workspace_bytes < pl.total || (pl.total > 0 && !workspace)) {
-    set_last_error("fused_moe: workspace too small (%zu < %zu)", workspace_bytes, pl.total);
-    return kWorkspaceTooSmall;
-  }
+  if ((st = check_layer_args(pl, activation, workspace, workspace_bytes)) != kOk) return st;
   if (num_tokens == 0) return kOk;
   if (!hidden || !w1 || !w2 || !topk_weights || !topk_ids || !out ||
       (quant != MSTAR_QUANT_NONE && (!w1_scale || !w2_scale))) {
     set_last_error("fused_moe: null tensor pointer");
     return kInvalidArgument;
   }
-  const int64_t M = num_tokens, H = hidden_size, I = inter;
-  const int E = num_experts;
   uint8_t* ws = (uint8_t*)workspace;
-  int32_t* sorted = (int32_t*)(ws + pl.off_sorted);
-  int32_t* eids = (int32_t*)(ws + pl.off_eids);
-  int32_t* ntpp = (int32_t*)(ws + pl.off_ntpp);
-  int32_t* eoff = (int32_t*)(ws + pl.off_eoff);
-  int32_t* ecnt = (int32_t*)(ws + pl.off_ecnt);
-  void* cache2 = ws + pl.off_c2;
-  void* cache3 = reduce_results ? (void*)(ws + pl.off_c3) : out;
-
-  st = launch_align(topk_ids, ids_dtype, pl.slots, E, pl.bm, sorted, eids, ntpp, pl.max_padded,
-                    eoff, ecnt, stream);
+  st = launch_align(topk_ids, ids_dtype, pl.slots, num_experts, pl.bm,
+                    (int32_t*)(ws + pl.off_sorted), (int32_t*)(ws + pl.off_eids),
+                    (int32_t*)(ws + pl.off_ntpp), pl.max_padded, (int32_t*)(ws + pl.off_eoff),
+                    (int32_t*)(ws + pl.off_ecnt), ws + pl.off_scratch, pl.scratch_bytes, stream);
   if (st != kOk) return st;
+  return run_experts(pl, hidden, act_dtype, num_tokens, hidden_size, w1, w2, num_experts, inter,
+                     quant, w1_scale, w2_scale, topk_weights, topk_w_dtype, top_k, activation,
+                     reduce_results, out, ws, stream);
+}
 
-  const int bkind = quant == MSTAR_QUANT_FP8_W8A8 ? B_FP8BLK : quant == MSTAR_QUANT_W4A16 ? B_INT4G : B_H16;
-  GemmArgs g1 = {};
-  g1.B = w1;
-  g1.C = cache2; g1.ldc = I;
-  g1.sorted_ids = sorted; g1.expert_ids = eids; g1.ntpp = ntpp;
-  g1.expert_off = eoff; g1.expert_cnt = ecnt;
-  g1.M = pl.slots; g1.N = (int)(2 * I); g1.K = (int)H; g1.top_k = top_k; g1.inter = (int)I;
-  g1.activation = activation; g1.num_experts = E; g1.m_blocks = (int)pl.max_blocks;
-  g1.topk_w = topk_weights; g1.topk_w_dtype = topk_w_dtype;
-  GemmArgs g2 = g1;
-  g2.B = w2;
-  g2.C = cache3; g2.ldc = H;
-  g2.N = (int)H; g2.K = (int)I; g2.top_k = 1; g2.mul_routed = 1;
-  g2.A = cache2; g2.lda = I;
+int mstar_moe_layer_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
+                                   int64_t inter, int top_k, int quant, int act_dtype,
+                                   size_t* bytes) {
+  Plan pl;
+  int st = make_plan(num_tokens, hidden, num_experts, inter, top_k, quant, act_dtype, 1, &pl, true);
+  if (st == kOk && bytes) *bytes = pl.total;
+  return st;
+}
 
-  if (bkind == B_FP8BLK) {
-    // w1: [E][2I][H] e4m3fn, scales [E][2I/128][H/128]; w2: [E][H][I], [E][H/128][I/128].
-    g1.ldb = H; g1.b_estride = 2 * I * H; g1.b_scale = w1_scale;
-    g1.bs_ld = H / 128; g1.bs_estride = (2 * I / 128) * (H / 128);
-    g2.ldb = I; g2.b_estride = H * I; g2.b_scale = w2_scale;
-    g2.bs_ld = I / 128; g2.bs_estride = (H / 128) * (I / 128);
-  } else if (bkind == B_INT4G) {
-    // w1: [E][2I][H/8] int32, scales [E][2I][H/128] bf16; w2: [E][H][I/8], [E][H][I/128].
-    g1.ldb = H / 8; g1.b_estride = 2 * I * (H / 8); g1.b_scale = w1_scale;
-    g1.bs_ld = H / 128; g1.bs_estride = 2 * I * (H / 128);
-    g2.ldb = I / 8; g2.b_estride = H * (I / 8); g2.b_scale = w2_scale;
-    g2.bs_ld = I / 128; g2.bs_estride = H * (I / 128);
-  } else {
-    g1.ldb = H; g1.b_estride = 2 * I * H;
-    g2.ldb = I; g2.b_estride = H * I;
+int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                    const void* router_logits, int logits_dtype, int renormalize, const void* w1,
+                    const void* w2, int num_experts, int64_t inter, int quant,
+                    const void* w1_scale, const void* w2_scale, int top_k, int activation,
+                    void* out, float* topk_weights_out, int64_t* topk_ids_out, void* workspace,
+                    size_t workspace_bytes, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  Plan pl;
+  int st = make_plan(num_tokens, hidden_size, num_experts, inter, top_k, quant, act_dtype, 1, &pl,
+                     true);
+  if (st != kOk) return st;
+  if ((st = check_layer_args(pl, activation, workspace, workspace_bytes)) != kOk) return st;
+  if (num_tokens == 0) return kOk;
+  if (!hidden || !router_logits || !w1 || !w2 || !out ||
+      (quant != MSTAR_QUANT_NONE && (!w1_scale || !w2_scale))) {
+    set_last_error("moe_layer: null tensor pointer");
+    return kInvalidArgument;
   }
+  uint8_t* ws = (uint8_t*)workspace;
+  float* tw = topk_weights_out ? topk_weights_out : (float*)(ws + pl.off_tw);
+  int32_t* ids32 = (int32_t*)(ws + pl.off_ids);
+  st = launch_route(router_logits, logits_dtype, num_tokens, num_experts, top_k, renormalize, tw,
+                    ids32, topk_ids_out, pl.bm, (int32_t*)(ws + pl.off_sorted),
+                    (int32_t*)(ws + pl.off_eids), (int32_t*)(ws + pl.off_ntpp), pl.max_padded,
+                    (int32_t*)(ws + pl.off_eoff), (int32_t*)(ws + pl.off_ecnt),
+                    ws + pl.off_scratch, pl.scratch_bytes, stream);
+  if (st != kOk) return st;
+  return run_experts(pl, hidden, act_dtype, num_tokens, hidden_size, w1, w2, num_experts, inter,
+                     quant, w1_scale, w2_scale, tw, kF32, top_k, activation, 1, out, ws, stream);
+}
 
-  if (pl.stream) {
-    g1.A = hidden; g1.lda = H;
-    st = launch_stream_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, (int)M, stream);
-    if (st != kOk) return st;
-    st = launch_stream_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, (int)M, stream);
-    if (st != kOk) return st;
-  } else if (bkind == B_FP8BLK) {
-    uint8_t* hq = ws + pl.off_hq;
-    float* hs = (float*)(ws + pl.off_hs);
-    uint8_t* cq = ws + pl.off_cq;
-    float* cs = (float*)(ws + pl.off_cs);
-    st = launch_quant_fp8_group(hidden, act_dtype, M, H, H, hq, hs, stream);
-    if (st != kOk) return st;
-    g1.A = hq; g1.lda = H; g1.a_scale = hs; g1.ld_as = H / 128;
-    st = launch_tile_gemm(g1, A_FP8G, B_FP8BLK, EPI_ACT, act_dtype, true, pl.bm, stream);
-    if (st != kOk) return st;
-    st = launch_quant_fp8_group(cache2, act_dtype, pl.slots, I, I, cq, cs, stream);
-    if (st != kOk) return st;
-    g2.A = cq; g2.lda = I; g2.a_scale = cs; g2.ld_as = I / 128;
-    st = launch_tile_gemm(g2, A_FP8G, B_FP8BLK, EPI_STORE, act_dtype, true, pl.bm, stream);
-    if (st != kOk) return st;
-  } else {
-    g1.A = hidden; g1.lda = H;
-    st = launch_tile_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, true, pl.bm, stream);
-    if (st != kOk) return st;
-    st = launch_tile_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, true, pl.bm, stream);
-    if (st != kOk) return st;
+int mstar_moe_route(const void* router_logits, int logits_dtype, int64_t num_tokens,
+                    int num_experts, int top_k, int renormalize, float* topk_weights,
+                    int32_t* topk_ids_i32, int64_t* topk_ids_i64, int block_size,
+                    int32_t* sorted_token_ids, int64_t sorted_len, int32_t* expert_ids,
+                    int64_t expert_ids_len, int32_t* num_tokens_post_pad, int32_t* expert_offsets,
+                    int32_t* expert_counts, void* scratch, size_t scratch_bytes, void* stream) {
+  if (block_size > 0 && expert_ids_len < (sorted_len + block_size - 1) / block_size) {
+    set_last_error("moe_route: experts_ids too small");
+    return kInvalidArgument;
   }
-  if (reduce_results)
-    return launch_sum_reduce(cache3, out, act_dtype, M, top_k, H, 1.0f, stream);
+  return launch_route(router_logits, logits_dtype, num_tokens, num_experts, top_k, renormalize,
+                      topk_weights, topk_ids_i32, topk_ids_i64, block_size, sorted_token_ids,
+                      expert_ids, num_tokens_post_pad, sorted_len, expert_offsets, expert_counts,
+                      scratch, scratch_bytes, (hipStream_t)stream);
+}
+
+int mstar_moe_route_scratch_size(int64_t num_tokens, int num_experts, int top_k, size_t* bytes) {
+  if (num_tokens < 0 || num_experts <= 0 || top_k <= 0) {
+    set_last_error("moe_route_scratch_size: invalid sizes");
+    return kInvalidArgument;
+  }
+  if (bytes) *bytes = route_scratch_bytes(num_tokens, top_k, num_experts);
+  return kOk;
+}
+
+int mstar_moe_align_scratch_size(int64_t numel, int num_experts, size_t* bytes) {
+  if (numel < 0 || num_experts <= 0) {
+    set_last_error("moe_align_scratch_size: invalid sizes");
+    return kInvalidArgument;
+  }
+  if (bytes) *bytes = align_scratch_bytes(numel, num_experts);
   return kOk;
 }
 

@@ -11,9 +11,22 @@ namespace mstar {
 // route.hip
 int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, int k,
                         int renorm, float* w, int32_t* ids32, int64_t* ids64, hipStream_t stream);
+// Alignment: one workgroup for numel <= 4096 (or without scratch), otherwise
+// a histogram pass and a scan+scatter pass over align_scratch_bytes() of
+// scratch.  Deterministic (slots ascend within an expert) either way.
 int launch_align(const void* ids, int ids_dtype, int64_t numel, int E, int bm,
                  int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, int64_t max_padded,
-                 int32_t* expert_off, int32_t* expert_cnt, hipStream_t stream);
+                 int32_t* expert_off, int32_t* expert_cnt, void* scratch, size_t scratch_bytes,
+                 hipStream_t stream);
+size_t align_scratch_bytes(int64_t numel, int E);
+// Softmax top-k + alignment: one launch for M*k <= 4096, else two
+// (top-k + per-workgroup histograms, then scan + scatter); the latter needs
+// route_scratch_bytes() of scratch.
+int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, int renorm,
+                 float* w, int32_t* ids32, int64_t* ids64, int bm, int32_t* sorted_ids,
+                 int32_t* expert_ids, int32_t* ntpp, int64_t max_padded, int32_t* expert_off,
+                 int32_t* expert_cnt, void* scratch, size_t scratch_bytes, hipStream_t stream);
+size_t route_scratch_bytes(int64_t M, int k, int E);
 
 // quant.hip
 int launch_quant_fp8_group(const void* x, int x_dtype, int64_t rows, int64_t cols,
@@ -77,8 +90,10 @@ int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dty
 bool stream_gemm_supported(int K, int max_rows, int akind, int bkind);
 
 // stream_fp8.hip: persistent FP8 weight streaming (bf16 activations,
-// quantised per 128-group on the fly).
-int launch_stream_fp8(const GemmArgs& a, int epi, hipStream_t stream);
+// quantised per 128-group on the fly).  exact: reduce each 128-block with
+// bf16 MFMAs on the exactly widened FP8 values (fp32-exact accumulation);
+// otherwise with the FP8 MFMA.
+int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream);
 bool stream_fp8_supported(int K, int N, int inter, int epi);
 
 }  // namespace mstar

@@ -603,6 +603,10 @@ static int dispatch_ks(const GemmArgs& a, hipStream_t s) {
   return kUnsupported;
 }
 
+// The decode path is bound by HBM, not by the MFMA rate, so it reduces the
+// FP8 products with the fp32-exact bf16 MFMA (see block_dot_fp8).
+constexpr bool kStreamExact = true;
+
 bool stream_gemm_supported(int K, int max_rows, int akind, int bkind) {
   (void)max_rows;
   if (K % 128 != 0) return false;
@@ -622,7 +626,7 @@ int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dty
     set_last_error("stream_gemm: missing expert offsets/counts or bad shapes");
     return kInvalidArgument;
   }
-  if (bkind == B_FP8BLK) return launch_stream_fp8(a, epi, stream);
+  if (bkind == B_FP8BLK) return launch_stream_fp8(a, epi, kStreamExact, stream);
   return epi == EPI_ACT ? dispatch_ks<B_INT4G, EPI_ACT>(a, stream)
                         : dispatch_ks<B_INT4G, EPI_STORE>(a, stream);
 }

@@ -25,17 +25,11 @@ __device__ inline float load_logit<uint16_t>(const uint16_t* p, int64_t i) {
   return bf16_bits_to_f32(p[i]);
 }
 
-// EPL = experts per lane (ceil(E / 64)).
+// Softmax top-k of one token by one wave (EPL = experts per lane,
+// ceil(E / 64)).  Lanes < k receive the t-th selected expert and weight.
 template <typename LT, int EPL>
-__global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict__ logits,
-                                                           int64_t M, int E, int k, int renorm,
-                                                           float* __restrict__ w_out,
-                                                           int32_t* __restrict__ ids32,
-                                                           int64_t* __restrict__ ids64) {
-  const int lane = threadIdx.x & 63;
-  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tok >= M) return;
-  const LT* row = logits + tok * E;
+__device__ __forceinline__ void topk_wave(const LT* __restrict__ row, int E, int k, int renorm, int lane,
+                                 int& out_id, float& out_w) {
   float v[EPL];
   float mx = -INFINITY;
 #pragma unroll
@@ -77,30 +71,59 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict_
     psum += p;
     if (lane == t) { sel_p = p; sel_id = bi; }
   }
+  out_id = sel_id;
+  out_w = renorm ? sel_p / psum : sel_p;
+}
+
+template <typename LT, int EPL>
+__global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict__ logits,
+                                                           int64_t M, int E, int k, int renorm,
+                                                           float* __restrict__ w_out,
+                                                           int32_t* __restrict__ ids32,
+                                                           int64_t* __restrict__ ids64) {
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= M) return;
+  int id;
+  float w;
+  topk_wave<LT, EPL>(logits + tok * E, E, k, renorm, lane, id, w);
   if (lane < k) {
-    float w = renorm ? sel_p / psum : sel_p;
     w_out[tok * k + lane] = w;
-    if (ids32) ids32[tok * k + lane] = sel_id;
-    if (ids64) ids64[tok * k + lane] = sel_id;
+    if (ids32) ids32[tok * k + lane] = id;
+    if (ids64) ids64[tok * k + lane] = id;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Alignment
+// Alignment building blocks (one 1024-thread workgroup = 16 waves)
 // ---------------------------------------------------------------------------
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
-constexpr int kAlignBatch = 16;  // ids held per lane per batch
+constexpr int kAlignBatch = 16;          // ids held per lane per batch
+constexpr int kRouteSmallSlots = 4096;   // numel served by one workgroup
+constexpr int kRouteTokensPerBlock = 128;
 
+// Expert of slot i, or E for "skip" (out of range / beyond the end).
 template <typename IT>
-__device__ inline int load_expert(const IT* ids, int64_t i, int64_t end, int E) {
-  if (i >= end) return E;
-  int64_t e = (int64_t)ids[i];
-  return (e < 0 || e >= E) ? E : (int)e;
-}
+struct GlobalIds {
+  const IT* ids;
+  __device__ int operator()(int64_t i, int64_t end, int E) const {
+    if (i >= end) return E;
+    const int64_t e = (int64_t)ids[i];
+    return (e < 0 || e >= E) ? E : (int)e;
+  }
+};
+struct LdsIds {
+  const int* ids;
+  __device__ int operator()(int64_t i, int64_t end, int E) const {
+    if (i >= end) return E;
+    const int e = ids[i];
+    return (e < 0 || e >= E) ? E : e;
+  }
+};
 
 // Lanes holding the same value as this lane (values in [0, 2^nbits)).
-__device__ inline uint64_t match_any(int v, int nbits) {
+__device__ __forceinline__ uint64_t match_any(int v, int nbits) {
   uint64_t m = ~0ull;
   for (int b = 0; b < nbits; ++b) {
     int bit = (v >> b) & 1;
@@ -110,74 +133,84 @@ __device__ inline uint64_t match_any(int v, int nbits) {
   return m;
 }
 
-template <typename IT>
-__global__ __launch_bounds__(kAlignThreads) void align_kernel(
-    const IT* __restrict__ ids, int64_t numel, int E, int bm, int32_t* __restrict__ sorted_ids,
-    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int64_t max_padded,
-    int32_t* __restrict__ expert_off, int32_t* __restrict__ expert_cnt) {
-  extern __shared__ int smem[];
-  int* cnt = smem;                        // [kAlignWaves][E]: counts, then running bases
-  int* off = cnt + kAlignWaves * E;       // [E + 1] padded exclusive offsets
-  int* tot = off + E + 1;                 // [E] real counts
-  int* wsum = tot + E;                    // [kAlignWaves] scan scratch
+// Each wave owns a contiguous 64-aligned sub-range of [s0, s1).
+__device__ __forceinline__ void wave_chunk(int64_t s0, int64_t s1, int w, int64_t& c0, int64_t& c1) {
+  const int64_t n = s1 - s0;
+  const int64_t chunk = ((n + kAlignWaves - 1) / kAlignWaves + 63) / 64 * 64;
+  c0 = s0 + (int64_t)w * chunk;
+  c1 = c0 + chunk < s1 ? c0 + chunk : s1;
+  if (c0 > s1) c0 = s1;
+}
+
+// wcnt[w * E + e] = number of slots of expert e in wave w's sub-range.
+// Leaders of equal-expert lane groups add the group size: no atomics.
+template <typename Load>
+__device__ __forceinline__ void range_counts(const Load& load, int64_t s0, int64_t s1, int E, int* wcnt) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int nbits = 32 - __builtin_clz((unsigned)E);  // values 0..E
-
-  for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) cnt[i] = 0;
+  const int nbits = 32 - __builtin_clz((unsigned)E);
+  for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wcnt[i] = 0;
   __syncthreads();
-
-  // Phase 1: per-wave histograms over contiguous chunks.
-  const int64_t chunk = ((numel + kAlignWaves - 1) / kAlignWaves + 63) / 64 * 64;
-  const int64_t c0 = (int64_t)w * chunk;
-  const int64_t c1 = c0 + chunk < numel ? c0 + chunk : numel;
-  int* mycnt = cnt + w * E;
+  int64_t c0, c1;
+  wave_chunk(s0, s1, w, c0, c1);
+  int* mycnt = wcnt + w * E;
   for (int64_t base = c0; base < c1; base += 64 * kAlignBatch) {
     int vals[kAlignBatch];
 #pragma unroll
-    for (int r = 0; r < kAlignBatch; ++r) vals[r] = load_expert(ids, base + r * 64 + lane, c1, E);
+    for (int r = 0; r < kAlignBatch; ++r) vals[r] = load(base + r * 64 + lane, c1, E);
 #pragma unroll
     for (int r = 0; r < kAlignBatch; ++r) {
       if (base + r * 64 >= c1) break;
-      uint64_t m = match_any(vals[r], nbits);
-      int leader = __builtin_ctzll(m);
-      if (lane == leader && vals[r] < E) mycnt[vals[r]] += __builtin_popcountll(m);
+      const uint64_t m = match_any(vals[r], nbits);
+      if (lane == __builtin_ctzll(m) && vals[r] < E) mycnt[vals[r]] += __builtin_popcountll(m);
     }
   }
   __syncthreads();
+}
 
-  // Phase 2: per expert, running bases across waves, padded counts, and an
-  // exclusive block scan of the padded counts.
-  int padded_local = 0;
-  for (int e = tid; e < E; e += kAlignThreads) {
+// Per expert: exclusive prefix of wcnt across waves (in place); tot[e] = sum.
+__device__ __forceinline__ void range_wave_prefix(int* wcnt, int E, int* tot) {
+  for (int e = threadIdx.x; e < E; e += kAlignThreads) {
     int run = 0;
     for (int ww = 0; ww < kAlignWaves; ++ww) {
-      int c = cnt[ww * E + e];
-      cnt[ww * E + e] = run;
+      const int c = wcnt[ww * E + e];
+      wcnt[ww * E + e] = run;
       run += c;
     }
     tot[e] = run;
-    padded_local = (run + bm - 1) / bm * bm;  // E <= kAlignThreads: one expert per thread
   }
-  int incl = wave_incl_scan(padded_local);
+  __syncthreads();
+}
+
+// off[0..E] = exclusive scan of roundup(cnt[e], bm).  E < 1024: one expert
+// per thread, wave scans plus a scan of the wave sums.
+__device__ __forceinline__ void expert_scan(const int* cnt, int E, int bm, int* off, int* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int padded = tid < E ? (cnt[tid] + bm - 1) / bm * bm : 0;
+  const int incl = wave_incl_scan(padded);
   if (lane == 63) wsum[w] = incl;
   __syncthreads();
   if (w == 0) {
-    int ws = lane < kAlignWaves ? wsum[lane] : 0;
-    int wi = wave_incl_scan(ws);
+    const int ws = lane < kAlignWaves ? wsum[lane] : 0;
+    const int wi = wave_incl_scan(ws);
     if (lane < kAlignWaves) wsum[lane] = wi - ws;
   }
   __syncthreads();
-  if (tid < E) off[tid] = wsum[w] + incl - padded_local;
+  if (tid < E) off[tid] = wsum[w] + incl - padded;
   if (tid == E - 1) off[E] = wsum[w] + incl;
   __syncthreads();
+}
+
+// expert_ids of every block, padding slots, the tail, and the extras.
+__device__ __forceinline__ void write_meta(const int* off, const int* tot, int E, int bm, int64_t numel,
+                           int64_t max_padded, int32_t* sorted_ids, int32_t* expert_ids,
+                           int32_t* ntpp, int32_t* expert_off, int32_t* expert_cnt) {
+  const int tid = threadIdx.x;
   const int total_padded = off[E];
   if (tid == 0) *ntpp = total_padded;
   if (expert_off)
     for (int e = tid; e <= E; e += kAlignThreads) expert_off[e] = off[e];
   if (expert_cnt)
     for (int e = tid; e < E; e += kAlignThreads) expert_cnt[e] = tot[e];
-
-  // Phase 3: expert_ids per block, padding positions, the tail.
   const int64_t max_blocks = (max_padded + bm - 1) / bm;
   for (int e = tid; e < E; e += kAlignThreads) {
     for (int i = off[e]; i < off[e + 1]; i += bm) expert_ids[i / bm] = e;
@@ -186,29 +219,182 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(
   for (int64_t i = total_padded / bm + tid; i < max_blocks; i += kAlignThreads) expert_ids[i] = 0;
   for (int64_t i = total_padded + tid; i < max_padded; i += kAlignThreads)
     sorted_ids[i] = (int32_t)numel;
+}
 
-  // Phase 4: stable scatter.  Within a wave, 64 consecutive slots per step;
-  // lanes with equal experts are ranked by lane order, and the leader bumps
-  // the wave's running base after everyone has read it.
-  for (int64_t base = c0; base < c1; base += 64 * kAlignBatch) {
+// Stable scatter of [s0, s1): slot i of expert e goes to
+// base[e] + (slots of e in earlier waves) + (earlier slots of e in this wave).
+template <typename Load>
+__device__ __forceinline__ void range_scatter(const Load& load, int64_t s0, int64_t s1, int E, const int* base,
+                              int* wcnt, int32_t* sorted_ids) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nbits = 32 - __builtin_clz((unsigned)E);
+  int64_t c0, c1;
+  wave_chunk(s0, s1, w, c0, c1);
+  int* mycnt = wcnt + w * E;
+  for (int64_t b0 = c0; b0 < c1; b0 += 64 * kAlignBatch) {
     int vals[kAlignBatch];
 #pragma unroll
-    for (int r = 0; r < kAlignBatch; ++r) vals[r] = load_expert(ids, base + r * 64 + lane, c1, E);
+    for (int r = 0; r < kAlignBatch; ++r) vals[r] = load(b0 + r * 64 + lane, c1, E);
 #pragma unroll
     for (int r = 0; r < kAlignBatch; ++r) {
-      if (base + r * 64 >= c1) break;
+      if (b0 + r * 64 >= c1) break;
       const int v = vals[r];
-      uint64_t m = match_any(v, nbits);
-      int rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
-      int b = v < E ? mycnt[v] : 0;
+      const uint64_t m = match_any(v, nbits);
+      const int rank = __builtin_popcountll(m & ((1ull << lane) - 1ull));
+      const int b = v < E ? mycnt[v] : 0;
       __builtin_amdgcn_wave_barrier();
       if (v < E) {
-        sorted_ids[off[v] + b + rank] = (int32_t)(base + r * 64 + lane);
+        sorted_ids[base[v] + b + rank] = (int32_t)(b0 + r * 64 + lane);
         if (rank == 0) mycnt[v] = b + __builtin_popcountll(m);
       }
       __builtin_amdgcn_wave_barrier();
     }
   }
+}
+
+// LDS layout of the single-workgroup paths (ints): wcnt[16E] off[E+1] tot[E] wsum[16]
+template <typename Load>
+__device__ __forceinline__ void single_block_align(int* smem, int64_t numel, int E, int bm,
+                                          int64_t max_padded, int32_t* sorted_ids,
+                                          int32_t* expert_ids, int32_t* ntpp,
+                                          int32_t* expert_off, int32_t* expert_cnt,
+                                          const Load& load) {
+  int* wcnt = smem;
+  int* off = wcnt + kAlignWaves * E;
+  int* tot = off + E + 1;
+  int* wsum = tot + E;
+  range_counts(load, 0, numel, E, wcnt);
+  range_wave_prefix(wcnt, E, tot);
+  expert_scan(tot, E, bm, off, wsum);
+  write_meta(off, tot, E, bm, numel, max_padded, sorted_ids, expert_ids, ntpp, expert_off,
+             expert_cnt);
+  range_scatter(load, 0, numel, E, off, wcnt, sorted_ids);
+}
+
+// moe_align_block_size in one workgroup (numel <= kRouteSmallSlots, or no
+// scratch for the grid-wide path).
+template <typename IT>
+__global__ __launch_bounds__(kAlignThreads) void align_kernel(
+    const IT* __restrict__ ids, int64_t numel, int E, int bm, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int64_t max_padded,
+    int32_t* __restrict__ expert_off, int32_t* __restrict__ expert_cnt) {
+  extern __shared__ int smem[];
+  single_block_align(smem, numel, E, bm, max_padded, sorted_ids, expert_ids, ntpp, expert_off,
+                     expert_cnt, GlobalIds<IT>{ids});
+}
+
+// Softmax top-k of every token plus the alignment, in one workgroup: the
+// decode-sized routing step is a single launch.
+template <typename LT, int EPL>
+__global__ __launch_bounds__(kAlignThreads) void route_small_kernel(
+    const LT* __restrict__ logits, int64_t M, int E, int k, int renorm, float* __restrict__ w_out,
+    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, int bm,
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp,
+    int64_t max_padded, int32_t* __restrict__ expert_off, int32_t* __restrict__ expert_cnt) {
+  extern __shared__ int smem[];
+  int* sIds = smem;                         // [M * k]
+  int* rest = sIds + ((M * k + 3) & ~3ll);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int64_t t = w; t < M; t += kAlignWaves) {
+    int id;
+    float wt;
+    topk_wave<LT, EPL>(logits + t * E, E, k, renorm, lane, id, wt);
+    if (lane < k) {
+      w_out[t * k + lane] = wt;
+      sIds[t * k + lane] = id;
+      if (ids32) ids32[t * k + lane] = id;
+      if (ids64) ids64[t * k + lane] = id;
+    }
+  }
+  __syncthreads();
+  single_block_align(rest, M * k, E, bm, max_padded, sorted_ids, expert_ids, ntpp, expert_off,
+                     expert_cnt, LdsIds{sIds});
+}
+
+// ---- grid-wide path --------------------------------------------------------
+// Pass 1 (top-k variant): top-k of kRouteTokensPerBlock tokens per workgroup
+// and the workgroup's expert histogram hist[b][E].
+template <typename LT, int EPL>
+__global__ __launch_bounds__(kAlignThreads) void topk_hist_kernel(
+    const LT* __restrict__ logits, int64_t M, int E, int k, int renorm, float* __restrict__ w_out,
+    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, int32_t* __restrict__ hist) {
+  extern __shared__ int smem[];
+  int* h = smem;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int e = threadIdx.x; e < E; e += kAlignThreads) h[e] = 0;
+  __syncthreads();
+  const int64_t t0 = (int64_t)blockIdx.x * kRouteTokensPerBlock;
+  for (int64_t t = t0 + w; t < t0 + kRouteTokensPerBlock && t < M; t += kAlignWaves) {
+    int id;
+    float wt;
+    topk_wave<LT, EPL>(logits + t * E, E, k, renorm, lane, id, wt);
+    if (lane < k) {
+      w_out[t * k + lane] = wt;
+      ids32[t * k + lane] = id;
+      if (ids64) ids64[t * k + lane] = id;
+      atomicAdd(&h[id], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kAlignThreads) hist[(int64_t)blockIdx.x * E + e] = h[e];
+}
+
+// Pass 1 (ids given): histogram of `per_block` slots per workgroup.
+template <typename IT>
+__global__ __launch_bounds__(kAlignThreads) void hist_kernel(const IT* __restrict__ ids,
+                                                             int64_t numel, int E, int per_block,
+                                                             int32_t* __restrict__ hist) {
+  extern __shared__ int smem[];
+  int* h = smem;
+  for (int e = threadIdx.x; e < E; e += kAlignThreads) h[e] = 0;
+  __syncthreads();
+  const int64_t s0 = (int64_t)blockIdx.x * per_block;
+  const GlobalIds<IT> load{ids};
+  for (int64_t i = s0 + threadIdx.x; i < s0 + per_block && i < numel; i += kAlignThreads) {
+    const int v = load(i, numel, E);
+    if (v < E) atomicAdd(&h[v], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kAlignThreads) hist[(int64_t)blockIdx.x * E + e] = h[e];
+}
+
+// Pass 2: every workgroup rebuilds the expert offsets from hist (identical
+// in all workgroups), workgroup 0 writes the metadata, and each workgroup
+// scatters its own slots after the slots of the workgroups before it.
+template <typename Load>
+__global__ __launch_bounds__(kAlignThreads) void scatter_kernel(
+    Load load, int64_t numel, int E, int bm, int per_block, int nblocks,
+    const int32_t* __restrict__ hist, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ ntpp, int64_t max_padded,
+    int32_t* __restrict__ expert_off, int32_t* __restrict__ expert_cnt) {
+  extern __shared__ int smem[];
+  int* wcnt = smem;                   // [16][E]
+  int* off = wcnt + kAlignWaves * E;  // [E+1]
+  int* tot = off + E + 1;             // [E]
+  int* base = tot + E;                // [E]
+  int* wsum = base + E;               // [16]
+  const int b = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += kAlignThreads) {
+    int pre = 0, all = 0;
+    for (int bb = 0; bb < nblocks; ++bb) {
+      const int c = hist[(int64_t)bb * E + e];
+      pre += bb < b ? c : 0;
+      all += c;
+    }
+    tot[e] = all;
+    base[e] = pre;
+  }
+  __syncthreads();
+  expert_scan(tot, E, bm, off, wsum);
+  if (b == 0)
+    write_meta(off, tot, E, bm, numel, max_padded, sorted_ids, expert_ids, ntpp, expert_off,
+               expert_cnt);
+  for (int e = threadIdx.x; e < E; e += kAlignThreads) base[e] += off[e];
+  const int64_t s0 = (int64_t)b * per_block;
+  const int64_t s1 = s0 + per_block < numel ? s0 + per_block : numel;
+  range_counts(load, s0, s1, E, wcnt);
+  range_wave_prefix(wcnt, E, tot);
+  range_scatter(load, s0, s1, E, base, wcnt, sorted_ids);
 }
 
 // ---------------------------------------------------------------------------
@@ -274,9 +460,23 @@ int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, 
 
 int align_max_padded(int64_t numel, int E, int bm) { return (int)(numel + (int64_t)E * (bm - 1)); }
 
-int launch_align(const void* ids, int ids_dtype, int64_t numel, int E, int bm,
-                 int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, int64_t max_padded,
-                 int32_t* expert_off, int32_t* expert_cnt, hipStream_t stream) {
+static size_t single_lds(int E) { return sizeof(int) * ((size_t)kAlignWaves * E + 2 * E + 1 + kAlignWaves); }
+static size_t scatter_lds(int E) { return sizeof(int) * ((size_t)kAlignWaves * E + 3 * E + 1 + kAlignWaves); }
+
+template <typename K>
+static int opt_in_lds(K kern, size_t bytes, size_t& done) {
+  if (bytes <= 64 * 1024 || bytes <= done) return kOk;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)bytes) != hipSuccess) {
+    set_last_error("routing: cannot reserve %zu bytes of LDS", bytes);
+    return kLaunchError;
+  }
+  done = bytes;
+  return kOk;
+}
+
+static int check_align_args(const void* ids, int64_t numel, int E, int bm, const int32_t* sorted_ids,
+                            const int32_t* expert_ids, const int32_t* ntpp, int64_t max_padded) {
   // Mirrors the checks of moe_align_block_size (moe_align_block_size.cu:211-224):
   // the padded expert count must stay below 1024 (one scan thread per expert).
   const int64_t padded_e = ((int64_t)E + 31) / 32 * 32;
@@ -295,31 +495,136 @@ int launch_align(const void* ids, int ids_dtype, int64_t numel, int E, int bm,
                    (long long)max_padded, (long long)(numel + (int64_t)E * (bm - 1)));
     return kInvalidArgument;
   }
+  return kOk;
+}
+
+size_t align_scratch_bytes(int64_t numel, int E) {
+  const int64_t blocks = (numel + kAlignThreads - 1) / kAlignThreads;
+  return (size_t)(blocks > 0 ? blocks : 1) * E * sizeof(int32_t);
+}
+
+size_t route_scratch_bytes(int64_t M, int k, int E) {
+  const int64_t blocks = (M + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock;
+  return (size_t)(blocks > 0 ? blocks : 1) * E * sizeof(int32_t) + (size_t)M * k * sizeof(int32_t);
+}
+
+int launch_align(const void* ids, int ids_dtype, int64_t numel, int E, int bm,
+                 int32_t* sorted_ids, int32_t* expert_ids, int32_t* ntpp, int64_t max_padded,
+                 int32_t* expert_off, int32_t* expert_cnt, void* scratch, size_t scratch_bytes,
+                 hipStream_t stream) {
+  int st = check_align_args(ids, numel, E, bm, sorted_ids, expert_ids, ntpp, max_padded);
+  if (st != kOk) return st;
   if (ids_dtype != kI32 && ids_dtype != kI64) {
     set_last_error("moe_align_block_size: topk_ids must be int32 or int64");
     return kUnsupported;
   }
-  size_t shmem = sizeof(int) * ((size_t)kAlignWaves * E + (E + 1) + E + kAlignWaves);
-  static size_t attr_bytes = 0;  // LDS beyond 64 KB needs an explicit opt-in
-  if (shmem > 64 * 1024 && shmem > attr_bytes) {
-    if (hipFuncSetAttribute((const void*)align_kernel<int32_t>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem) != hipSuccess ||
-        hipFuncSetAttribute((const void*)align_kernel<int64_t>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem) != hipSuccess) {
-      set_last_error("moe_align_block_size: cannot reserve %zu bytes of LDS", shmem);
-      return kLaunchError;
+  const bool grid_path = numel > kRouteSmallSlots && scratch &&
+                         scratch_bytes >= align_scratch_bytes(numel, E);
+  if (!grid_path) {
+    const size_t shmem = single_lds(E);
+    static size_t done32 = 0, done64 = 0;
+    if (ids_dtype == kI32) {
+      if ((st = opt_in_lds(align_kernel<int32_t>, shmem, done32)) != kOk) return st;
+      align_kernel<int32_t><<<1, kAlignThreads, shmem, stream>>>(
+          (const int32_t*)ids, numel, E, bm, sorted_ids, expert_ids, ntpp, max_padded, expert_off,
+          expert_cnt);
+    } else {
+      if ((st = opt_in_lds(align_kernel<int64_t>, shmem, done64)) != kOk) return st;
+      align_kernel<int64_t><<<1, kAlignThreads, shmem, stream>>>(
+          (const int64_t*)ids, numel, E, bm, sorted_ids, expert_ids, ntpp, max_padded, expert_off,
+          expert_cnt);
     }
-    attr_bytes = shmem;
+    return launch_status("moe_align_block_size");
   }
-  if (ids_dtype == kI32)
-    align_kernel<int32_t><<<1, kAlignThreads, shmem, stream>>>(
-        (const int32_t*)ids, numel, E, bm, sorted_ids, expert_ids, ntpp, max_padded, expert_off,
-        expert_cnt);
-  else
-    align_kernel<int64_t><<<1, kAlignThreads, shmem, stream>>>(
-        (const int64_t*)ids, numel, E, bm, sorted_ids, expert_ids, ntpp, max_padded, expert_off,
-        expert_cnt);
+  const int nblocks = (int)((numel + kAlignThreads - 1) / kAlignThreads);
+  int32_t* hist = (int32_t*)scratch;
+  const size_t hshm = E * sizeof(int), sshm = scatter_lds(E);
+  static size_t d1 = 0, d2 = 0, d3 = 0, d4 = 0;
+  if (ids_dtype == kI32) {
+    hist_kernel<int32_t><<<nblocks, kAlignThreads, hshm, stream>>>((const int32_t*)ids, numel, E,
+                                                                   kAlignThreads, hist);
+    if ((st = opt_in_lds(scatter_kernel<GlobalIds<int32_t>>, sshm, d1)) != kOk) return st;
+    scatter_kernel<<<nblocks, kAlignThreads, sshm, stream>>>(
+        GlobalIds<int32_t>{(const int32_t*)ids}, numel, E, bm, kAlignThreads, nblocks, hist,
+        sorted_ids, expert_ids, ntpp, max_padded, expert_off, expert_cnt);
+  } else {
+    hist_kernel<int64_t><<<nblocks, kAlignThreads, hshm, stream>>>((const int64_t*)ids, numel, E,
+                                                                   kAlignThreads, hist);
+    if ((st = opt_in_lds(scatter_kernel<GlobalIds<int64_t>>, sshm, d2)) != kOk) return st;
+    scatter_kernel<<<nblocks, kAlignThreads, sshm, stream>>>(
+        GlobalIds<int64_t>{(const int64_t*)ids}, numel, E, bm, kAlignThreads, nblocks, hist,
+        sorted_ids, expert_ids, ntpp, max_padded, expert_off, expert_cnt);
+  }
+  (void)d3;
+  (void)d4;
   return launch_status("moe_align_block_size");
+}
+
+template <typename LT, int EPL>
+static int route_impl(const void* logits, int64_t M, int E, int k, int renorm, float* w,
+                      int32_t* ids32, int64_t* ids64, int bm, int32_t* sorted_ids,
+                      int32_t* expert_ids, int32_t* ntpp, int64_t max_padded, int32_t* expert_off,
+                      int32_t* expert_cnt, void* scratch, size_t scratch_bytes,
+                      hipStream_t stream) {
+  const int64_t numel = M * k;
+  int st;
+  if (numel <= kRouteSmallSlots) {
+    const size_t shmem = sizeof(int) * (size_t)((numel + 3) & ~3ll) + single_lds(E);
+    static size_t done = 0;
+    if ((st = opt_in_lds(route_small_kernel<LT, EPL>, shmem, done)) != kOk) return st;
+    route_small_kernel<LT, EPL><<<1, kAlignThreads, shmem, stream>>>(
+        (const LT*)logits, M, E, k, renorm, w, ids32, ids64, bm, sorted_ids, expert_ids, ntpp,
+        max_padded, expert_off, expert_cnt);
+    return launch_status("moe_route");
+  }
+  if (!scratch || scratch_bytes < route_scratch_bytes(M, k, E)) {
+    set_last_error("moe_route: scratch too small (%zu < %zu)", scratch_bytes,
+                   route_scratch_bytes(M, k, E));
+    return kWorkspaceTooSmall;
+  }
+  const int nblocks = (int)((M + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock);
+  int32_t* hist = (int32_t*)scratch;
+  int32_t* tmp_ids = ids32 ? ids32 : hist + (size_t)nblocks * E;
+  topk_hist_kernel<LT, EPL><<<nblocks, kAlignThreads, E * sizeof(int), stream>>>(
+      (const LT*)logits, M, E, k, renorm, w, tmp_ids, ids64, hist);
+  const size_t sshm = scatter_lds(E);
+  static size_t done = 0;
+  if ((st = opt_in_lds(scatter_kernel<GlobalIds<int32_t>>, sshm, done)) != kOk) return st;
+  scatter_kernel<<<nblocks, kAlignThreads, sshm, stream>>>(
+      GlobalIds<int32_t>{tmp_ids}, numel, E, bm, kRouteTokensPerBlock * k, nblocks, hist,
+      sorted_ids, expert_ids, ntpp, max_padded, expert_off, expert_cnt);
+  return launch_status("moe_route");
+}
+
+int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, int renorm,
+                 float* w, int32_t* ids32, int64_t* ids64, int bm, int32_t* sorted_ids,
+                 int32_t* expert_ids, int32_t* ntpp, int64_t max_padded, int32_t* expert_off,
+                 int32_t* expert_cnt, void* scratch, size_t scratch_bytes, hipStream_t stream) {
+  if (M < 0 || k <= 0 || k > 64 || k > E || !w || (M > 0 && !logits)) {
+    set_last_error("moe_route: invalid arguments (M=%lld E=%d k=%d)", (long long)M, E, k);
+    return kInvalidArgument;
+  }
+  int st = check_align_args(logits, M * k, E, bm, sorted_ids, expert_ids, ntpp, max_padded);
+  if (st != kOk) return st;
+  if (logits_dtype != kF32 && logits_dtype != kBF16) {
+    set_last_error("moe_route: logits must be float32 or bfloat16");
+    return kUnsupported;
+  }
+  const int epl = (E + 63) / 64;
+#define MSTAR_ROUTE(N)                                                                          \
+  return logits_dtype == kF32                                                                   \
+             ? route_impl<float, N>(logits, M, E, k, renorm, w, ids32, ids64, bm, sorted_ids,   \
+                                    expert_ids, ntpp, max_padded, expert_off, expert_cnt,       \
+                                    scratch, scratch_bytes, stream)                             \
+             : route_impl<uint16_t, N>(logits, M, E, k, renorm, w, ids32, ids64, bm,            \
+                                       sorted_ids, expert_ids, ntpp, max_padded, expert_off,    \
+                                       expert_cnt, scratch, scratch_bytes, stream);
+  if (epl <= 1) { MSTAR_ROUTE(1) }
+  if (epl <= 2) { MSTAR_ROUTE(2) }
+  if (epl <= 4) { MSTAR_ROUTE(4) }
+  if (epl <= 8) { MSTAR_ROUTE(8) }
+  MSTAR_ROUTE(16)
+#undef MSTAR_ROUTE
 }
 
 }  // namespace mstar

@@ -40,7 +40,39 @@ __device__ inline v8i lds_v8i(const uint8_t* p) {
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-template <int EPI, int KS>
+// Eight e4m3fn bytes (two dwords) -> one bf16x8 MFMA operand, exactly
+// (e4m3fn is a subset of bf16).  Whole 32-bit pairs are moved: pulling
+// single __bf16 elements out of the packed result makes the compiler insert
+// byte permutes that scramble the pairs.
+__device__ inline v8s fp8x8_to_bf16x8(int x0, int x1) {
+  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+  const int c0 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x0, 1.0f, false));
+  const int c1 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x0, 1.0f, true));
+  const int c2 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x1, 1.0f, false));
+  const int c3 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x1, 1.0f, true));
+  return __builtin_bit_cast(v8s, v4i{c0, c1, c2, c3});
+}
+
+// One 16x16x128 block product of e4m3fn fragments.  EXACT: the fragments
+// are widened to bf16 (exactly) and reduced by four chained bf16 MFMAs,
+// whose fp32 accumulation is exact to fp32 rounding; otherwise one
+// v_mfma_f32_16x16x128_f8f6f4, whose internal reduction of the 128
+// products keeps fewer bits (partial sums can be off by ~1e-5 relative).
+template <bool EXACT>
+__device__ inline v4f block_dot_fp8(const v8i& a, const v8i& b) {
+  if constexpr (!EXACT) {
+    return mfma_fp8_16x16x128(a, b, v4f{0.f, 0.f, 0.f, 0.f});
+  } else {
+    v4f t = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      t = mfma_bf16_16x16x32(fp8x8_to_bf16x8(a[2 * s], a[2 * s + 1]),
+                             fp8x8_to_bf16x8(b[2 * s], b[2 * s + 1]), t);
+    return t;
+  }
+}
+
+template <int EPI, int KS, bool EXACT>
 __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
   constexpr int K = KS * 128;
   constexpr int KC = KS % 4 == 0 ? 4 : (KS % 3 == 0 ? 3 : KS);  // K steps loaded at once
@@ -163,7 +195,7 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
             const int kg = c * KC + kk;
             v8i af = arow_ok ? lds_v8i(sA + l16 * LDA + kg * 128 + lg * 32)
                              : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-            v4f t = mfma_fp8_16x16x128(af, b[kk], v4f{0.f, 0.f, 0.f, 0.f});
+            v4f t = block_dot_fp8<EXACT>(af, b[kk]);
             v4f sa = *(const v4f*)(sAs + kg * RC + lg * 4);
             acc += t * (sa * sw[kk]);
           }
@@ -208,12 +240,12 @@ static int num_cu() {
   return g_num_cu;
 }
 
-template <int EPI, int KS>
+template <int EPI, int KS, bool EXACT>
 static int run_stream_fp8(const GemmArgs& a, hipStream_t stream) {
   constexpr int K = KS * 128;
   const size_t shmem = (size_t)kStreamRows * (K + 16) + (size_t)KS * kStreamRows * 4 +
                        kStreamRows * 4 + (size_t)a.num_experts * 4;
-  auto kern = stream_fp8_kernel<EPI, KS>;
+  auto kern = stream_fp8_kernel<EPI, KS, EXACT>;
   static size_t attr_bytes = 0;  // largest LDS size opted in so far
   if (shmem > attr_bytes) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -236,15 +268,18 @@ bool stream_fp8_supported(int K, int N, int inter, int epi) {
   return ks_ok && n_ok;
 }
 
-int launch_stream_fp8(const GemmArgs& a, int epi, hipStream_t stream) {
+int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream) {
   if (!stream_fp8_supported(a.K, a.N, a.inter, epi) || a.num_experts > 1024) {
     set_last_error("stream_fp8: unsupported shape (K=%d N=%d)", a.K, a.N);
     return kUnsupported;
   }
 #define MSTAR_SF8(KS)                                                                       \
   case KS:                                                                                  \
-    return epi == EPI_ACT ? run_stream_fp8<EPI_ACT, KS>(a, stream)                          \
-                          : run_stream_fp8<EPI_STORE, KS>(a, stream);
+    if (exact)                                                                              \
+      return epi == EPI_ACT ? run_stream_fp8<EPI_ACT, KS, true>(a, stream)                  \
+                            : run_stream_fp8<EPI_STORE, KS, true>(a, stream);               \
+    return epi == EPI_ACT ? run_stream_fp8<EPI_ACT, KS, false>(a, stream)                   \
+                          : run_stream_fp8<EPI_STORE, KS, false>(a, stream);
   switch (a.K / 128) {
     MSTAR_SF8(1)
     MSTAR_SF8(2)

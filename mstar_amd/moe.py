@@ -67,6 +67,11 @@ class _Experts(nn.Module):
         self.quant = mode
 
 
+def _quant_code(mode: str | None) -> int:
+    from ._lib import QUANT_FP8_W8A8, QUANT_NONE, QUANT_W4A16
+    return {None: QUANT_NONE, "fp8_w8a8": QUANT_FP8_W8A8, "w4a16": QUANT_W4A16}[mode]
+
+
 def dispatch(hidden_states, experts: _Experts, num_experts, selected_experts, routing_weights):
     return fused_experts(hidden_states, experts.gate_up_proj, experts.down_proj, routing_weights,
                          selected_experts, quant=experts.quant, w1_scale=experts.w1_scale,
@@ -90,11 +95,26 @@ class SparseMoeBlock(nn.Module):
         self.experts.quantize(mode)
         return self
 
+    def routed(self, flat, router_states=None):
+        """Routed experts of ``flat [T, H]`` -> ``(out, router_states_next)``.
+        With the default router the gate projection stays an ``F.linear``
+        and everything after it (softmax top-k, align, both GEMMs, the
+        top-k sum) is one library call."""
+        if type(self.gate) is TopKRouter:
+            logits = F.linear(flat, self.gate.weight)
+            ex = self.experts
+            out, _, _ = ops.moe_layer(flat, logits, ex.gate_up_proj, ex.down_proj, self.gate.top_k,
+                                      self.gate.norm_topk_prob, 0, _quant_code(ex.quant),
+                                      ex.w1_scale, ex.w2_scale)
+            return out, None
+        w, ids, router_states_next = self.gate(flat, router_states)
+        return dispatch(flat, self.experts, self.num_experts, ids, w), router_states_next
+
     def forward(self, hidden_states, router_states=None, *, return_router_states: bool = False):
         input_shape = hidden_states.shape
         flat = hidden_states.view(-1, hidden_states.shape[-1]).contiguous()
-        w, ids, router_states_next = self.gate(flat, router_states)
-        out = dispatch(flat, self.experts, self.num_experts, ids, w).view(input_shape)
+        out, router_states_next = self.routed(flat, router_states)
+        out = out.view(input_shape)
         return (out, router_states_next) if return_router_states else out
 
 
@@ -113,7 +133,6 @@ class SparseMoeBlockWithSharedExpert(SparseMoeBlock):
         input_shape = hidden_states.shape
         flat = hidden_states.view(-1, hidden_states.shape[-1]).contiguous()
         shared = self.shared_expert(flat)
-        w, ids, router_states_next = self.gate(flat, router_states)
-        routed = dispatch(flat, self.experts, self.num_experts, ids, w)
+        routed, router_states_next = self.routed(flat, router_states)
         out = (routed + torch.sigmoid(self.shared_expert_gate(flat)) * shared).view(input_shape)
         return (out, router_states_next) if return_router_states else out

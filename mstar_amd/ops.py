@@ -60,10 +60,14 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int,
     sorted_ids = torch.empty(max_padded, dtype=torch.int32, device=dev)
     expert_ids = torch.empty(max_blocks, dtype=torch.int32, device=dev)
     ntpp = torch.empty(1, dtype=torch.int32, device=dev)
-    check(load().mstar_moe_align_block_size(
+    lib = load()
+    nb = ctypes.c_size_t(0)
+    check(lib.mstar_moe_align_scratch_size(numel, num_experts, ctypes.byref(nb)), "moe_align_block_size")
+    scratch = torch.empty(max(nb.value, 4), dtype=torch.uint8, device=dev)
+    check(lib.mstar_moe_align_block_size(
         ptr(topk_ids), dtype_code(topk_ids.dtype), numel, num_experts, block_size,
         ptr(sorted_ids), max_padded, ptr(expert_ids), max_blocks, ptr(ntpp), None, None,
-        stream_of(topk_ids)), "moe_align_block_size")
+        ptr(scratch), nb.value, stream_of(topk_ids)), "moe_align_block_size")
     return sorted_ids, expert_ids, ntpp
 
 
@@ -74,6 +78,46 @@ def _(topk_ids, block_size, num_experts):
     return (topk_ids.new_empty(max_padded, dtype=torch.int32),
             topk_ids.new_empty(max_blocks, dtype=torch.int32),
             topk_ids.new_empty(1, dtype=torch.int32))
+
+
+@torch.library.custom_op(f"{_NS}::moe_route", mutates_args=())
+def moe_route(logits: torch.Tensor, top_k: int, renormalize: bool, block_size: int
+              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Softmax top-k and alignment in one call: (weights fp32, ids int64,
+    sorted_token_ids, expert_ids, num_tokens_post_padded)."""
+    _lib.require_gpu(logits)
+    logits = logits.contiguous()
+    M, E = logits.shape
+    numel = M * top_k
+    max_padded = numel + E * (block_size - 1)
+    max_blocks = -(-max_padded // block_size)
+    dev = logits.device
+    w = torch.empty(M, top_k, dtype=torch.float32, device=dev)
+    ids = torch.empty(M, top_k, dtype=torch.int64, device=dev)
+    sorted_ids = torch.empty(max_padded, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(max_blocks, dtype=torch.int32, device=dev)
+    ntpp = torch.empty(1, dtype=torch.int32, device=dev)
+    lib = load()
+    nb = ctypes.c_size_t(0)
+    check(lib.mstar_moe_route_scratch_size(M, E, top_k, ctypes.byref(nb)), "moe_route")
+    scratch = torch.empty(max(nb.value, 4), dtype=torch.uint8, device=dev)
+    check(lib.mstar_moe_route(ptr(logits), dtype_code(logits.dtype), M, E, top_k, int(renormalize),
+                              ptr(w), None, ptr(ids), block_size, ptr(sorted_ids), max_padded,
+                              ptr(expert_ids), max_blocks, ptr(ntpp), None, None, ptr(scratch),
+                              nb.value, stream_of(logits)), "moe_route")
+    return w, ids, sorted_ids, expert_ids, ntpp
+
+
+@moe_route.register_fake
+def _(logits, top_k, renormalize, block_size):
+    M, E = logits.shape
+    max_padded = M * top_k + E * (block_size - 1)
+    max_blocks = -(-max_padded // block_size)
+    return (logits.new_empty(M, top_k, dtype=torch.float32),
+            logits.new_empty(M, top_k, dtype=torch.int64),
+            logits.new_empty(max_padded, dtype=torch.int32),
+            logits.new_empty(max_blocks, dtype=torch.int32),
+            logits.new_empty(1, dtype=torch.int32))
 
 
 # --------------------------------------------------------------- elementwise
@@ -177,6 +221,40 @@ def _(hidden, w1, w2, topk_weights, topk_ids, activation, reduce_results, quant,
     if reduce_results:
         return hidden.new_empty(M, H)
     return hidden.new_empty(M, topk_ids.shape[1], H)
+
+
+@torch.library.custom_op(f"{_NS}::moe_layer", mutates_args=())
+def moe_layer(hidden: torch.Tensor, router_logits: torch.Tensor, w1: torch.Tensor,
+              w2: torch.Tensor, top_k: int, renormalize: bool, activation: int, quant: int,
+              w1_scale: Optional[torch.Tensor], w2_scale: Optional[torch.Tensor]
+              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Routed MoE layer from router logits: (out, topk_weights fp32, topk_ids int64)."""
+    _lib.require_gpu(hidden, router_logits, w1, w2)
+    dummy_ids = torch.empty(hidden.shape[0], top_k, dtype=torch.int64, device=hidden.device)
+    dummy_w = torch.empty(hidden.shape[0], top_k, dtype=torch.float32, device=hidden.device)
+    M, H, E, inter = _check_fused_args(hidden, w1, w2, dummy_w, dummy_ids, quant, w1_scale, w2_scale)
+    logits = router_logits.contiguous()
+    if logits.shape != (M, E):
+        raise ValueError(f"moe_layer: router_logits must be [{M}, {E}]")
+    lib = load()
+    act_dt = dtype_code(hidden.dtype)
+    nbytes = ctypes.c_size_t(0)
+    check(lib.mstar_moe_layer_workspace_size(M, H, E, inter, top_k, quant, act_dt,
+                                             ctypes.byref(nbytes)), "moe_layer")
+    ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=hidden.device)
+    out = torch.empty(M, H, dtype=hidden.dtype, device=hidden.device)
+    check(lib.mstar_moe_layer(
+        ptr(hidden), act_dt, M, H, ptr(logits), dtype_code(logits.dtype), int(renormalize), ptr(w1),
+        ptr(w2), E, inter, quant, ptr(w1_scale), ptr(w2_scale), top_k, activation, ptr(out),
+        ptr(dummy_w), ptr(dummy_ids), ptr(ws), nbytes.value, stream_of(hidden)), "moe_layer")
+    return out, dummy_w, dummy_ids
+
+
+@moe_layer.register_fake
+def _(hidden, router_logits, w1, w2, top_k, renormalize, activation, quant, w1_scale, w2_scale):
+    M, H = hidden.shape
+    return (hidden.new_empty(M, H), hidden.new_empty(M, top_k, dtype=torch.float32),
+            hidden.new_empty(M, top_k, dtype=torch.int64))
 
 
 # ---------------------------------------------------------- FP8 quant / GEMM

@@ -18,11 +18,16 @@ def moe_errors(out: torch.Tensor, ref: torch.Tensor):
     return float(err.max() / scale), float(err.mean() / rms)
 
 
+# (what, max_rel, mean_abs/rms) of every comparison, written out by conftest.
+RECORDS: list = []
+
+
 def assert_moe_close(out: torch.Tensor, ref: torch.Tensor, max_rel=MAX_REL,
                      mean_of_rms=MEAN_ABS_OF_RMS, what=""):
     assert out.shape == ref.shape, (out.shape, ref.shape)
     assert torch.isfinite(out.float()).all(), f"{what}: non-finite output"
     mr, ma = moe_errors(out, ref)
+    RECORDS.append({"what": what, "max_rel": mr, "mean_abs_over_rms": ma})
     assert mr <= max_rel and ma <= mean_of_rms, (
         f"{what}: max_rel={mr:.3e} (<= {max_rel}), mean_abs/rms={ma:.3e} (<= {mean_of_rms})")
 

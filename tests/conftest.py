@@ -25,3 +25,13 @@ def pytest_collection_modifyitems(config, items):
 @pytest.fixture(autouse=True)
 def _seed():
     torch.manual_seed(0)
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """Write the measured parity errors next to the GPU run's other outputs."""
+    from tests._util import RECORDS
+    out_dir = os.path.join(ROOT, "gpurun_out")
+    if RECORDS and torch.cuda.is_available() and os.path.isdir(out_dir):
+        import json
+        with open(os.path.join(out_dir, "parity_errors.json"), "w") as f:
+            json.dump(RECORDS, f, indent=1)

@@ -54,7 +54,7 @@ def _err():
 def test_align_rejects_too_many_experts():
     lib = _lib.load()
     st = lib.mstar_moe_align_block_size(None, _lib.DT_I32, 0, 1024, 16, None, 0, None, 0, None,
-                                        None, None, None)
+                                        None, None, None, 0, None)
     assert st == 1 and "less than 1024" in _err()
 
 
@@ -62,7 +62,7 @@ def test_align_rejects_small_output():
     lib = _lib.load()
     buf = ctypes.c_void_p(8)  # never dereferenced: validation fails first
     st = lib.mstar_moe_align_block_size(buf, _lib.DT_I32, 256, 128, 16, buf, 100, buf, 1000, buf,
-                                        None, None, None)
+                                        None, None, None, 0, None)
     assert st == 1 and "too small" in _err()
 
 
@@ -88,6 +88,22 @@ def test_workspace_too_small_is_reported():
     st = lib.mstar_fused_moe(p, _lib.DT_BF16, 32, 2048, p, p, 128, 768, 0, None, None, p,
                              _lib.DT_F32, p, _lib.DT_I32, 8, 0, 1, p, p, 16, None)
     assert st == 4 and "workspace too small" in _err()
+
+
+def test_layer_and_route_sizes():
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    assert lib.mstar_moe_layer_workspace_size(32, 2048, 128, 768, 8, _lib.QUANT_FP8_W8A8,
+                                              _lib.DT_BF16, ctypes.byref(n)) == 0
+    assert n.value > 0
+    assert lib.mstar_moe_route_scratch_size(8192, 128, 8, ctypes.byref(n)) == 0
+    assert n.value >= 64 * 128 * 4
+    assert lib.mstar_moe_align_scratch_size(65536, 128, ctypes.byref(n)) == 0
+    assert n.value == 64 * 128 * 4
+    p = ctypes.c_void_p(256)
+    st = lib.mstar_moe_route(p, _lib.DT_F32, 8192, 128, 8, 1, p, None, None, 64, p, 100, p, 10, p,
+                             None, None, None, 0, None)
+    assert st == 1 and "too small" in _err()
 
 
 def test_topk_rejects_bad_k():

@@ -290,3 +290,40 @@ def test_layer_under_hip_graph_replays():
             assert torch.equal(out, eager)
             _ = fn()  # eager work between replays
             torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,bias,quant", [(32, False, "fp8_w8a8"), (8, False, "fp8_w8a8"),
+                                          (512, True, "fp8_w8a8"), (16, False, None),
+                                          (32, False, "w4a16")])
+def test_moe_layer_from_logits(M, bias, quant):
+    """Routing from logits + experts in one library call (mstar_moe_layer)."""
+    from mstar_amd import _lib, ops, quant as Q
+    H, E, I, k = 2048, 128, 768, 8
+    x = _hidden(M, H, seed=M + 21)
+    g = torch.Generator().manual_seed(M + 22)
+    logits = torch.randn(M, E, generator=g)
+    if bias:
+        logits = logits + O.zipf_bias(E)
+    rw, rids = O.router_topk_softmax(logits, k, True)
+    w1, w2 = _weights(H, E, I)
+    if quant == "fp8_w8a8":
+        q1, s1, q2, s2 = _fp8_weights(H, E, I)
+        out, tw, ti = ops.moe_layer(x.to(DEV), logits.to(DEV), q1, q2, k, True, 0,
+                                    _lib.QUANT_FP8_W8A8, s1, s2)
+        ref = _fp8_ref(x, q1, s1, q2, s2, rw, rids)
+    elif quant == "w4a16":
+        p1, t1 = Q.quantize_int4_group(w1)
+        p2, t2 = Q.quantize_int4_group(w2)
+        out, tw, ti = ops.moe_layer(x.to(DEV), logits.to(DEV), p1, p2, k, True, 0,
+                                    _lib.QUANT_W4A16, t1, t2)
+        p1c, t1c, p2c, t2c = p1.cpu(), t1.cpu(), p2.cpu(), t2.cpu()
+        ref = O.fused_experts_rounding(x, None, None, rw, rids,
+                                       w1_dq=lambda e: O.dequant_int4_group(p1c[e], t1c[e]),
+                                       w2_dq=lambda e: O.dequant_int4_group(p2c[e], t2c[e]))
+    else:
+        out, tw, ti = ops.moe_layer(x.to(DEV), logits.to(DEV), w1, w2, k, True, 0,
+                                    _lib.QUANT_NONE, None, None)
+        ref = O.fused_experts_rounding(x, w1.cpu(), w2.cpu(), rw, rids)
+    assert torch.equal(ti.cpu(), rids)
+    torch.testing.assert_close(tw.cpu(), rw, rtol=2e-6, atol=1e-9)
+    assert_moe_close(out, ref, what=f"moe_layer M={M} {quant}")

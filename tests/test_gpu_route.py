@@ -102,3 +102,28 @@ def test_align_all_tokens_one_expert():
     rs, re_, rn = O.moe_align_block_size(ids.numpy(), 64, 128)
     assert np.array_equal(s.cpu().numpy(), rs) and np.array_equal(e.cpu().numpy(), re_)
     assert int(n.cpu()) == int(rn[0])
+
+
+@pytest.mark.parametrize("M,E,k,bm,bias,dt", [
+    (32, 128, 8, 16, False, torch.float32),      # decode: one launch
+    (512, 128, 8, 64, True, torch.float32),      # exactly 4096 slots: one launch
+    (600, 128, 8, 64, True, torch.float32),      # grid path, ragged last block
+    (8192, 128, 8, 64, True, torch.float32),     # config 3 prefill
+    (1000, 64, 6, 32, False, torch.bfloat16),    # bf16 logits (ties), k=6
+    (3, 8, 2, 64, False, torch.float32),
+])
+def test_route_fused_vs_oracle(M, E, k, bm, bias, dt):
+    from mstar_amd import ops
+    gen = torch.Generator().manual_seed(M + E + k)
+    logits = torch.randn(M, E, generator=gen)
+    if bias:
+        logits = logits + O.zipf_bias(E)
+    logits = logits.to(dt)
+    w, ids, s, e, n = ops.moe_route(logits.to(DEV), k, True, bm)
+    rw, rids = O.router_topk_softmax(logits.float(), k, True)
+    assert torch.equal(ids.cpu(), rids)
+    torch.testing.assert_close(w.cpu(), rw, rtol=2e-6, atol=1e-9)
+    rs, re_, rn = O.moe_align_block_size(rids.numpy(), bm, E)
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(e.cpu().numpy(), re_)
+    assert np.array_equal(n.cpu().numpy(), rn)
