@@ -38,10 +38,11 @@ static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Row block for the tiled grouped GEMM: about one block per expert's share of
 // the slots, so padding stays a small fraction of the work.
-static int choose_bm(int64_t slots, int E) {
+static int choose_bm(int64_t slots, int E, bool fp8) {
   const int64_t avg = slots / (E > 0 ? E : 1);
   if (avg <= 48) return 32;
   if (avg <= 160) return 64;
+  if (fp8 && avg >= 256) return kBigBlockM;
   return 128;
 }
 
@@ -83,7 +84,7 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->stream = quant != MSTAR_QUANT_NONE && M <= kStreamMaxTokens &&
                stream_gemm_supported((int)H, (int)M, A_H16, bkind) &&
                stream_gemm_supported((int)I, (int)M, A_H16, bkind);
-  pl->bm = pl->stream ? 16 : choose_bm(pl->slots, E);
+  pl->bm = pl->stream ? 16 : choose_bm(pl->slots, E, quant == MSTAR_QUANT_FP8_W8A8);
   pl->max_padded = pl->slots + (int64_t)E * (pl->bm - 1);
   pl->max_blocks = (pl->max_padded + pl->bm - 1) / pl->bm;
   size_t o = 0;
@@ -278,7 +279,7 @@ int mstar_fp8_scaled_mm(const uint8_t* a, const float* a_scale, const uint8_t* w
   g.B = w; g.ldb = K; g.b_estride = 0; g.b_scale = w_scale;
   g.C = out; g.ldc = N;
   g.M = M; g.N = (int)N; g.K = (int)K; g.top_k = 1;
-  const int bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+  const int bm = M <= 32 ? 32 : M <= 64 ? 64 : kBigBlockM;
   return launch_tile_gemm(g, A_FP8R, B_FP8R, EPI_DENSE, kBF16, false, bm, (hipStream_t)stream);
 }
 

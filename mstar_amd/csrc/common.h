@@ -121,6 +121,13 @@ __device__ inline int wave_incl_scan(int v) {
 __device__ inline v4f mfma_fp8_16x16x128(v8i a, v8i b, v4f c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
+// 32x32x64 FP8: lane l supplies row/column (l % 32) and 32 consecutive K
+// bytes at K offset (l / 32) * 32.  Result: lane l, register i holds
+// C[8*(i/4) + 4*(l/32) + (i%4)][l % 32].
+typedef float v16f __attribute__((ext_vector_type(16)));
+__device__ inline v16f mfma_fp8_32x32x64(v8i a, v8i b, v16f c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
 // 16x16x32 bf16 / fp16: lane l supplies row (l % 16) and 8 consecutive K
 // elements at K offset (l / 16) * 8.  Same C layout as above.
 __device__ inline v4f mfma_bf16_16x16x32(v8s a, v8s b, v4f c) {

@@ -89,6 +89,11 @@ int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dty
                        int max_rows, hipStream_t stream);
 bool stream_gemm_supported(int K, int max_rows, int akind, int bkind);
 
+// gemm_fp8.hip: 256 x 128 tile FP8 GEMM (8 waves, double-buffered LDS);
+// grouped needs the alignment block size 256.
+int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t stream);
+constexpr int kBigBlockM = 256;
+
 // stream_fp8.hip: persistent FP8 weight streaming (bf16 activations,
 // quantised per 128-group on the fly).  exact: reduce each 128-block with
 // bf16 MFMAs on the exactly widened FP8 values (fp32-exact accumulation);

@@ -25,54 +25,98 @@ __device__ inline float load_logit<uint16_t>(const uint16_t* p, int64_t i) {
   return bf16_bits_to_f32(p[i]);
 }
 
+// Order-preserving map fp32 -> uint32 (larger float, larger key).
+__device__ __forceinline__ uint32_t float_key(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // Softmax top-k of one token by one wave (EPL = experts per lane,
-// ceil(E / 64)).  Lanes < k receive the t-th selected expert and weight.
-template <typename LT, int EPL>
-__device__ __forceinline__ void topk_wave(const LT* __restrict__ row, int E, int k, int renorm, int lane,
-                                 int& out_id, float& out_w) {
+// ceil(E / 64); expert e sits in lane e % 64, slot e / 64).
+//
+// Selection is a radix select on order-preserving integer keys of the
+// logits (softmax is monotonic, so ranking logits ranks probabilities): 32
+// MSB-first steps, each one ballot + popcount per slot, find the k-th
+// largest key T; keys > T are selected, and of the keys == T the lowest
+// expert indices fill the rest.  Output ranks (value descending, ties by
+// index) come from k scalar broadcasts.  No cross-lane shuffles except the
+// three reductions (max, sum, selected sum) of the softmax.
+// emit(rank, expert, weight) is called once per selected expert.
+template <typename LT, int EPL, typename Emit>
+__device__ __forceinline__ void topk_wave(const LT* __restrict__ row, int E, int k, int renorm,
+                                          int lane, const Emit& emit) {
   float v[EPL];
+  uint32_t key[EPL];
+  bool valid[EPL];
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    int e = j * 64 + lane;
-    v[j] = e < E ? load_logit<LT>(row, e) : -INFINITY;
+    const int e = j * 64 + lane;
+    valid[j] = e < E;
+    v[j] = valid[j] ? load_logit<LT>(row, e) : -INFINITY;
+    key[j] = valid[j] ? float_key(v[j]) : 0u;
     mx = fmaxf(mx, v[j]);
   }
   mx = wave_max(mx);
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    int e = j * 64 + lane;
-    if (e < E) s += __expf(v[j] - mx);
-  }
+  for (int j = 0; j < EPL; ++j) s += valid[j] ? __expf(v[j] - mx) : 0.f;
   s = wave_sum(s);
-  unsigned taken = 0;  // bit j: v[j] already selected
-  float sel_p = 0.f, psum = 0.f;
-  int sel_id = 0;
-  for (int t = 0; t < k; ++t) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+
+  // ---- radix select of the k-th largest key
+  uint32_t prefix = 0;
+  int need = k;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t hi_mask = 0xFFFFFFFFu << bit;
+    const uint32_t cand = prefix | (1u << bit);
+    int cnt = 0;
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      int e = j * 64 + lane;
-      bool ok = e < E && !((taken >> j) & 1u);
-      if (ok && (v[j] > bv || bi == 0x7fffffff)) { bv = v[j]; bi = e; }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      float ov = __shfl_xor(bv, o, 64);
-      int oi = __shfl_xor(bi, o, 64);
-      bool take = (oi != 0x7fffffff) &&
-                  (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-      if (take) { bv = ov; bi = oi; }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    float p = __expf(bv - mx) / s;
-    psum += p;
-    if (lane == t) { sel_p = p; sel_id = bi; }
+    for (int j = 0; j < EPL; ++j) cnt += __builtin_popcountll(__ballot(valid[j] && (key[j] & hi_mask) == cand));
+    if (cnt >= need) prefix = cand;
+    else need -= cnt;
   }
-  out_id = sel_id;
-  out_w = renorm ? sel_p / psum : sel_p;
+  // ---- selection: keys above T, then `need` ties at T by ascending index
+  const uint64_t lt = (1ull << lane) - 1ull;
+  bool sel[EPL];
+  int ties_before = 0;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const bool eq = valid[j] && key[j] == prefix;
+    const uint64_t beq = __ballot(eq);
+    const int tie_rank = ties_before + __builtin_popcountll(beq & lt);
+    sel[j] = valid[j] && (key[j] > prefix || (eq && tie_rank < need));
+    ties_before += __builtin_popcountll(beq);
+  }
+  // ---- output rank of each selected expert
+  int rank[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) rank[j] = 0;
+#pragma unroll
+  for (int j2 = 0; j2 < EPL; ++j2) {
+    uint64_t m = __ballot(sel[j2]);
+    while (m) {
+      const int src = __builtin_ctzll(m);
+      m &= m - 1ull;
+      const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)key[j2], src);
+      const int is = j2 * 64 + src;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) {
+        const int idx = j * 64 + lane;
+        rank[j] += (ks > key[j] || (ks == key[j] && is < idx)) ? 1 : 0;
+      }
+    }
+  }
+  float p[EPL];
+  float psum = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    p[j] = sel[j] ? __expf(v[j] - mx) / s : 0.f;
+    psum += p[j];
+  }
+  if (renorm) psum = wave_sum(psum);
+#pragma unroll
+  for (int j = 0; j < EPL; ++j)
+    if (sel[j]) emit(rank[j], j * 64 + lane, renorm ? p[j] / psum : p[j]);
 }
 
 template <typename LT, int EPL>
@@ -84,14 +128,11 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict_
   const int lane = threadIdx.x & 63;
   const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= M) return;
-  int id;
-  float w;
-  topk_wave<LT, EPL>(logits + tok * E, E, k, renorm, lane, id, w);
-  if (lane < k) {
-    w_out[tok * k + lane] = w;
-    if (ids32) ids32[tok * k + lane] = id;
-    if (ids64) ids64[tok * k + lane] = id;
-  }
+  topk_wave<LT, EPL>(logits + tok * E, E, k, renorm, lane, [&](int r, int id, float w) {
+    w_out[tok * k + r] = w;
+    if (ids32) ids32[tok * k + r] = id;
+    if (ids64) ids64[tok * k + r] = id;
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -296,15 +337,12 @@ __global__ __launch_bounds__(kAlignThreads) void route_small_kernel(
   int* rest = sIds + ((M * k + 3) & ~3ll);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int64_t t = w; t < M; t += kAlignWaves) {
-    int id;
-    float wt;
-    topk_wave<LT, EPL>(logits + t * E, E, k, renorm, lane, id, wt);
-    if (lane < k) {
-      w_out[t * k + lane] = wt;
-      sIds[t * k + lane] = id;
-      if (ids32) ids32[t * k + lane] = id;
-      if (ids64) ids64[t * k + lane] = id;
-    }
+    topk_wave<LT, EPL>(logits + t * E, E, k, renorm, lane, [&](int r, int id, float wt) {
+      w_out[t * k + r] = wt;
+      sIds[t * k + r] = id;
+      if (ids32) ids32[t * k + r] = id;
+      if (ids64) ids64[t * k + r] = id;
+    });
   }
   __syncthreads();
   single_block_align(rest, M * k, E, bm, max_padded, sorted_ids, expert_ids, ntpp, expert_off,
@@ -325,15 +363,12 @@ __global__ __launch_bounds__(kAlignThreads) void topk_hist_kernel(
   __syncthreads();
   const int64_t t0 = (int64_t)blockIdx.x * kRouteTokensPerBlock;
   for (int64_t t = t0 + w; t < t0 + kRouteTokensPerBlock && t < M; t += kAlignWaves) {
-    int id;
-    float wt;
-    topk_wave<LT, EPL>(logits + t * E, E, k, renorm, lane, id, wt);
-    if (lane < k) {
-      w_out[t * k + lane] = wt;
-      ids32[t * k + lane] = id;
-      if (ids64) ids64[t * k + lane] = id;
+    topk_wave<LT, EPL>(logits + t * E, E, k, renorm, lane, [&](int r, int id, float wt) {
+      w_out[t * k + r] = wt;
+      ids32[t * k + r] = id;
+      if (ids64) ids64[t * k + r] = id;
       atomicAdd(&h[id], 1);
-    }
+    });
   }
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += kAlignThreads) hist[(int64_t)blockIdx.x * E + e] = h[e];

@@ -75,7 +75,7 @@ __device__ inline v4f block_dot_fp8(const v8i& a, const v8i& b) {
 template <int EPI, int KS, bool EXACT>
 __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
   constexpr int K = KS * 128;
-  constexpr int KC = KS % 4 == 0 ? 4 : (KS % 3 == 0 ? 3 : KS);  // K steps loaded at once
+  constexpr int KC = KS <= 6 ? KS : (KS % 4 == 0 ? 4 : (KS % 3 == 0 ? 3 : KS));  // K steps loaded at once
   constexpr int CH = KS / KC;                                   // loads per item
   constexpr int LDA = K + 16;
   constexpr int RC = kStreamRows;

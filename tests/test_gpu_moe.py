@@ -327,3 +327,15 @@ def test_moe_layer_from_logits(M, bias, quant):
     assert torch.equal(ti.cpu(), rids)
     torch.testing.assert_close(tw.cpu(), rw, rtol=2e-6, atol=1e-9)
     assert_moe_close(out, ref, what=f"moe_layer M={M} {quant}")
+
+
+@pytest.mark.parametrize("M,E,k,H,I,bias", [(1024, 16, 4, 512, 256, False), (2048, 32, 8, 1024, 384, True)])
+def test_fused_experts_fp8_big_tile_path(M, E, k, H, I, bias):
+    """>= 256 slots per expert on average selects the 256 x 128 FP8 tile kernel."""
+    from mstar_amd.fused_moe import fused_experts
+    q1, s1, q2, s2 = _fp8_weights(H, E, I, seed=9)
+    x = _hidden(M, H, seed=9)
+    tw, ti = _routing(M, E, k, seed=9, bias=bias)
+    out = fused_experts(x.to(DEV), q1, q2, tw.to(DEV), ti.to(DEV), quant="fp8_w8a8",
+                        w1_scale=s1, w2_scale=s2)
+    assert_moe_close(out, _fp8_ref(x, q1, s1, q2, s2, tw, ti), what=f"fp8 big tile M={M}")
