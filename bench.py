@@ -42,6 +42,15 @@ FP8_PEAK_TFLOPS = 5000.0
 EXPERT_FP8_BYTES = 2 * INTER * H + H * INTER                      # 4,718,592
 EXPERT_SCALE_BYTES = ((2 * INTER // 128) * (H // 128) + (H // 128) * (INTER // 128)) * 4  # 1,152
 W_COPIES = 4
+COPY_BYTES = 512 << 20
+# HBM traffic of one gate_up launch at config 2 (seed 0, 115 hit experts),
+# from two rocprofv3 --pmc passes over `bench.py --kernel-only` (FETCH_SIZE,
+# then WRITE_SIZE; KiB per dispatch, mean of 24 dispatches).  Each counter
+# is scaled by what it reads for torch's neg kernel over COPY_BYTES in the
+# same run: FETCH_SIZE reports 262,153.5 KiB for the 524,288 KiB read
+# (x2.0), WRITE_SIZE 524,288 KiB for the 524,288 KiB written (x1.0).
+GATE_UP_FETCH_KIB, FETCH_FACTOR = 179044.1, 2.0
+GATE_UP_WRITE_KIB, WRITE_FACTOR = 594.0, 1.0
 
 
 def parse():
@@ -219,8 +228,15 @@ def main():
     x, logits = make_inputs(M, bias=False)
 
     if args.kernel_only:
+        # Also one plain elementwise pass that reads and writes COPY_BYTES
+        # (torch's neg kernel, named NegFunctor in traces): the calibration
+        # kernel for the FETCH_SIZE / WRITE_SIZE counters under rocprofv3 --pmc.
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
         us = gate_up_kernel_timing(x, logits, weights, args.steps, args.warmup)
-        print(json.dumps({"gate_up_us": us}))
+        print(json.dumps({"gate_up_us": us, "copy_bytes": COPY_BYTES}))
         return
 
     graphs = []
@@ -237,6 +253,7 @@ def main():
     g1_bytes = hits * (2 * INTER * H + (2 * INTER // 128) * (H // 128) * 4) + M * H * 2 + M * K_TOP * INTER * 2
     g1_gbs = g1_bytes / (k_us * 1e-6) / 1e9
 
+    traffic = int(GATE_UP_FETCH_KIB * 1024 * FETCH_FACTOR + GATE_UP_WRITE_KIB * 1024 * WRITE_FACTOR)
     out = {
         "metric": "fused FP8 MoE layer us + % HBM/MFMA roofline at M=32 and M=8192",
         "value": round(us, 2),
@@ -255,9 +272,10 @@ def main():
                    "hit_experts": hits, "weight_copies_rotated": W_COPIES},
         "layer": {"us": round(us, 2), "algorithmic_bytes": layer_bytes, "GBps": round(layer_gbs, 1),
                   "hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
-        "roofline": {"kernel": "stream_gemm_kernel (gate_up + SiLU-and-mul)", "bound": "hbm",
+        "roofline": {"kernel": "stream_fp8_kernel<EPI_ACT> (gate_up + SiLU-and-mul)", "bound": "hbm",
                      "achieved": round(g1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g1_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(g1_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic if M == 32 else None,
                      "bytes_per_launch": g1_bytes, "us_per_launch": round(k_us, 3)},
     }
 
