@@ -51,6 +51,9 @@ constexpr int64_t kStreamMaxTokens = 64;
 
 struct Plan {
   bool stream = false;
+  // FP8 weight streaming with the slot lists built inside the GEMMs from the
+  // router ids: no alignment launch.
+  bool ids_mode = false;
   int bm = 16;
   int64_t slots = 0, max_padded = 0, max_blocks = 0;
   size_t off_sorted, off_eids, off_ntpp, off_eoff, off_ecnt, off_c2, off_c3, off_hq, off_hs,
@@ -84,6 +87,7 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->stream = quant != MSTAR_QUANT_NONE && M <= kStreamMaxTokens &&
                stream_gemm_supported((int)H, (int)M, A_H16, bkind) &&
                stream_gemm_supported((int)I, (int)M, A_H16, bkind);
+  pl->ids_mode = pl->stream && quant == MSTAR_QUANT_FP8_W8A8 && pl->slots <= kStreamMaxIdsSlots;
   pl->bm = pl->stream ? 16 : choose_bm(pl->slots, E, quant == MSTAR_QUANT_FP8_W8A8);
   pl->max_padded = pl->slots + (int64_t)E * (pl->bm - 1);
   pl->max_blocks = (pl->max_padded + pl->bm - 1) / pl->bm;
@@ -127,8 +131,9 @@ static int check_layer_args(const Plan& pl, int activation, void* workspace, siz
 static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_t num_tokens,
                        int64_t hidden_size, const void* w1, const void* w2, int num_experts,
                        int64_t inter, int quant, const void* w1_scale, const void* w2_scale,
-                       const void* topk_weights, int topk_w_dtype, int top_k, int activation,
-                       int reduce_results, void* out, uint8_t* ws, hipStream_t stream) {
+                       const void* topk_weights, int topk_w_dtype, const void* topk_ids,
+                       int ids_dtype, int top_k, int activation, int reduce_results, void* out,
+                       uint8_t* ws, hipStream_t stream) {
   const int64_t M = num_tokens, H = hidden_size, I = inter;
   const int E = num_experts;
   int st = kOk;
@@ -148,6 +153,7 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
   g1.M = pl.slots; g1.N = (int)(2 * I); g1.K = (int)H; g1.top_k = top_k; g1.inter = (int)I;
   g1.activation = activation; g1.num_experts = E; g1.m_blocks = (int)pl.max_blocks;
   g1.topk_w = topk_weights; g1.topk_w_dtype = topk_w_dtype;
+  if (pl.ids_mode) { g1.topk_ids = topk_ids; g1.ids_dtype = ids_dtype; }
   GemmArgs g2 = g1;
   g2.B = w2;
   g2.C = cache3; g2.ldc = H;
@@ -399,15 +405,21 @@ int mstar_fused_moe(const void* hidden, int act_dtype, int64_t num_tokens, int64
     set_last_error("fused_moe: null tensor pointer");
     return kInvalidArgument;
   }
+  if (ids_dtype != kI32 && ids_dtype != kI64) {
+    set_last_error("fused_moe: topk_ids must be int32 or int64");
+    return kUnsupported;
+  }
   uint8_t* ws = (uint8_t*)workspace;
-  st = launch_align(topk_ids, ids_dtype, pl.slots, num_experts, pl.bm,
-                    (int32_t*)(ws + pl.off_sorted), (int32_t*)(ws + pl.off_eids),
-                    (int32_t*)(ws + pl.off_ntpp), pl.max_padded, (int32_t*)(ws + pl.off_eoff),
-                    (int32_t*)(ws + pl.off_ecnt), ws + pl.off_scratch, pl.scratch_bytes, stream);
-  if (st != kOk) return st;
+  if (!pl.ids_mode) {
+    st = launch_align(topk_ids, ids_dtype, pl.slots, num_experts, pl.bm,
+                      (int32_t*)(ws + pl.off_sorted), (int32_t*)(ws + pl.off_eids),
+                      (int32_t*)(ws + pl.off_ntpp), pl.max_padded, (int32_t*)(ws + pl.off_eoff),
+                      (int32_t*)(ws + pl.off_ecnt), ws + pl.off_scratch, pl.scratch_bytes, stream);
+    if (st != kOk) return st;
+  }
   return run_experts(pl, hidden, act_dtype, num_tokens, hidden_size, w1, w2, num_experts, inter,
-                     quant, w1_scale, w2_scale, topk_weights, topk_w_dtype, top_k, activation,
-                     reduce_results, out, ws, stream);
+                     quant, w1_scale, w2_scale, topk_weights, topk_w_dtype, topk_ids, ids_dtype,
+                     top_k, activation, reduce_results, out, ws, stream);
 }
 
 int mstar_moe_layer_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
@@ -440,14 +452,19 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
   uint8_t* ws = (uint8_t*)workspace;
   float* tw = topk_weights_out ? topk_weights_out : (float*)(ws + pl.off_tw);
   int32_t* ids32 = (int32_t*)(ws + pl.off_ids);
-  st = launch_route(router_logits, logits_dtype, num_tokens, num_experts, top_k, renormalize, tw,
-                    ids32, topk_ids_out, pl.bm, (int32_t*)(ws + pl.off_sorted),
-                    (int32_t*)(ws + pl.off_eids), (int32_t*)(ws + pl.off_ntpp), pl.max_padded,
-                    (int32_t*)(ws + pl.off_eoff), (int32_t*)(ws + pl.off_ecnt),
-                    ws + pl.off_scratch, pl.scratch_bytes, stream);
+  if (pl.ids_mode)
+    st = launch_topk_softmax(router_logits, logits_dtype, num_tokens, num_experts, top_k,
+                             renormalize, tw, ids32, topk_ids_out, stream);
+  else
+    st = launch_route(router_logits, logits_dtype, num_tokens, num_experts, top_k, renormalize, tw,
+                      ids32, topk_ids_out, pl.bm, (int32_t*)(ws + pl.off_sorted),
+                      (int32_t*)(ws + pl.off_eids), (int32_t*)(ws + pl.off_ntpp), pl.max_padded,
+                      (int32_t*)(ws + pl.off_eoff), (int32_t*)(ws + pl.off_ecnt),
+                      ws + pl.off_scratch, pl.scratch_bytes, stream);
   if (st != kOk) return st;
   return run_experts(pl, hidden, act_dtype, num_tokens, hidden_size, w1, w2, num_experts, inter,
-                     quant, w1_scale, w2_scale, tw, kF32, top_k, activation, 1, out, ws, stream);
+                     quant, w1_scale, w2_scale, tw, kF32, ids32, kI32, top_k, activation, 1, out,
+                     ws, stream);
 }
 
 int mstar_moe_route(const void* router_logits, int logits_dtype, int64_t num_tokens,

@@ -77,6 +77,11 @@ struct GemmArgs {
   int activation;     // 0 silu, 1 gelu
   int num_experts;
   int m_blocks;       // grouped: number of m-blocks (expert_ids length)
+  // Streaming FP8 kernels only: when set, the per-expert slot lists are
+  // built from these [M] router ids (int32 or int64, ids_dtype) instead of
+  // sorted_ids / expert_off / expert_cnt.
+  const void* topk_ids;
+  int ids_dtype;
 };
 
 // Tiled grouped / dense GEMM (LDS-staged MFMA tiles); bm is the row block.
@@ -99,6 +104,7 @@ constexpr int kBigBlockM = 256;
 // bf16 MFMAs on the exactly widened FP8 values (fp32-exact accumulation);
 // otherwise with the FP8 MFMA.
 int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream);
+constexpr int64_t kStreamMaxIdsSlots = 1024;  // slots a launch in ids mode can take
 bool stream_fp8_supported(int K, int N, int inter, int epi);
 
 }  // namespace mstar

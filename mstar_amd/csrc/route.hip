@@ -42,10 +42,10 @@ __device__ __forceinline__ uint32_t float_key(float v) {
 // index) come from k scalar broadcasts.  No cross-lane shuffles except the
 // three reductions (max, sum, selected sum) of the softmax.
 // emit(rank, expert, weight) is called once per selected expert.
-template <typename LT, int EPL, typename Emit>
-__device__ __forceinline__ void topk_wave(const LT* __restrict__ row, int E, int k, int renorm,
-                                          int lane, const Emit& emit) {
-  float v[EPL];
+// v[j] holds the logit of expert j * 64 + lane (-inf past E).
+template <int EPL, typename Emit>
+__device__ __forceinline__ void topk_wave(const float (&v)[EPL], int E, int k, int renorm, int lane,
+                                          const Emit& emit) {
   uint32_t key[EPL];
   bool valid[EPL];
   float mx = -INFINITY;
@@ -53,7 +53,6 @@ __device__ __forceinline__ void topk_wave(const LT* __restrict__ row, int E, int
   for (int j = 0; j < EPL; ++j) {
     const int e = j * 64 + lane;
     valid[j] = e < E;
-    v[j] = valid[j] ? load_logit<LT>(row, e) : -INFINITY;
     key[j] = valid[j] ? float_key(v[j]) : 0u;
     mx = fmaxf(mx, v[j]);
   }
@@ -119,6 +118,37 @@ __device__ __forceinline__ void topk_wave(const LT* __restrict__ row, int E, int
     if (sel[j]) emit(rank[j], j * 64 + lane, renorm ? p[j] / psum : p[j]);
 }
 
+// Top-k of tokens t0, t0 + stride, ... (< t1) by one wave, a batch at a
+// time: the logit rows of a batch are loaded together, so the wave waits
+// for memory once per batch instead of once per token (batch size shrinks
+// with the experts per lane to stay within 128 VGPRs).
+// emit(token, rank, expert, weight).
+template <typename LT, int EPL, typename Emit>
+__device__ __forceinline__ void topk_tokens(const LT* __restrict__ logits, int64_t t0, int64_t t1,
+                                            int64_t stride, int E, int k, int renorm, int lane,
+                                            const Emit& emit) {
+  constexpr int kTopkBatch = EPL >= 8 ? 1 : (EPL >= 4 ? 2 : 4);
+  for (int64_t tb = t0; tb < t1; tb += kTopkBatch * stride) {
+    float v[kTopkBatch][EPL];
+#pragma unroll
+    for (int b = 0; b < kTopkBatch; ++b) {
+      const int64_t t = tb + b * stride;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) {
+        const int e = j * 64 + lane;
+        v[b][j] = (t < t1 && e < E) ? load_logit<LT>(logits + t * E, e) : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kTopkBatch; ++b) {
+      const int64_t t = tb + b * stride;
+      if (t >= t1) break;
+      topk_wave<EPL>(v[b], E, k, renorm, lane,
+                     [&](int r, int id, float w) { emit(t, r, id, w); });
+    }
+  }
+}
+
 template <typename LT, int EPL>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict__ logits,
                                                            int64_t M, int E, int k, int renorm,
@@ -126,9 +156,15 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict_
                                                            int32_t* __restrict__ ids32,
                                                            int64_t* __restrict__ ids64) {
   const int lane = threadIdx.x & 63;
-  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tok = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (tok >= M) return;
-  topk_wave<LT, EPL>(logits + tok * E, E, k, renorm, lane, [&](int r, int id, float w) {
+  float v[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = j * 64 + lane;
+    v[j] = e < E ? load_logit<LT>(logits + tok * E, e) : -INFINITY;
+  }
+  topk_wave<EPL>(v, E, k, renorm, lane, [&](int r, int id, float w) {
     w_out[tok * k + r] = w;
     if (ids32) ids32[tok * k + r] = id;
     if (ids64) ids64[tok * k + r] = id;
@@ -336,14 +372,13 @@ __global__ __launch_bounds__(kAlignThreads) void route_small_kernel(
   int* sIds = smem;                         // [M * k]
   int* rest = sIds + ((M * k + 3) & ~3ll);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int64_t t = w; t < M; t += kAlignWaves) {
-    topk_wave<LT, EPL>(logits + t * E, E, k, renorm, lane, [&](int r, int id, float wt) {
-      w_out[t * k + r] = wt;
-      sIds[t * k + r] = id;
-      if (ids32) ids32[t * k + r] = id;
-      if (ids64) ids64[t * k + r] = id;
-    });
-  }
+  topk_tokens<LT, EPL>(logits, w, M, kAlignWaves, E, k, renorm, lane,
+                       [&](int64_t t, int r, int id, float wt) {
+                         w_out[t * k + r] = wt;
+                         sIds[t * k + r] = id;
+                         if (ids32) ids32[t * k + r] = id;
+                         if (ids64) ids64[t * k + r] = id;
+                       });
   __syncthreads();
   single_block_align(rest, M * k, E, bm, max_padded, sorted_ids, expert_ids, ntpp, expert_off,
                      expert_cnt, LdsIds{sIds});
@@ -362,14 +397,14 @@ __global__ __launch_bounds__(kAlignThreads) void topk_hist_kernel(
   for (int e = threadIdx.x; e < E; e += kAlignThreads) h[e] = 0;
   __syncthreads();
   const int64_t t0 = (int64_t)blockIdx.x * kRouteTokensPerBlock;
-  for (int64_t t = t0 + w; t < t0 + kRouteTokensPerBlock && t < M; t += kAlignWaves) {
-    topk_wave<LT, EPL>(logits + t * E, E, k, renorm, lane, [&](int r, int id, float wt) {
-      w_out[t * k + r] = wt;
-      ids32[t * k + r] = id;
-      if (ids64) ids64[t * k + r] = id;
-      atomicAdd(&h[id], 1);
-    });
-  }
+  const int64_t t1 = t0 + kRouteTokensPerBlock < M ? t0 + kRouteTokensPerBlock : M;
+  topk_tokens<LT, EPL>(logits, t0 + w, t1, kAlignWaves, E, k, renorm, lane,
+                       [&](int64_t t, int r, int id, float wt) {
+                         w_out[t * k + r] = wt;
+                         ids32[t * k + r] = id;
+                         if (ids64) ids64[t * k + r] = id;
+                         atomicAdd(&h[id], 1);
+                       });
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += kAlignThreads) hist[(int64_t)blockIdx.x * E + e] = h[e];
 }
@@ -448,7 +483,11 @@ int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, 
     return kUnsupported;
   }
   if (M == 0) return kOk;
-  dim3 grid((unsigned)((M + 3) / 4)), block(256);
+  // One wave per token.  Small batches get one-wave workgroups, so the
+  // tokens spread over as many CUs as possible (the radix select is a long
+  // dependent chain; one SIMD per token keeps it at issue latency).
+  const int wpb = M <= 2048 ? 1 : 4;
+  dim3 grid((unsigned)((M + wpb - 1) / wpb)), block(64 * wpb);
   const int epl = (E + 63) / 64;
 #define MSTAR_TOPK_CASE(N)                                                                   \
   case N:                                                                                    \

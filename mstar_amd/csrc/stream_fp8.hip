@@ -34,6 +34,7 @@ namespace mstar {
 constexpr int kStreamRows = 16;   // token rows staged per pass (one MFMA row block)
 constexpr int kStreamWaves = 4;   // waves per workgroup
 constexpr int kStreamWgPerCu = 4; // resident workgroups per CU (LDS ~35 KB each)
+constexpr int kStreamSlotsPerThread = 4;  // ids mode: up to 1024 slots per launch
 
 __device__ inline v8i lds_v8i(const uint8_t* p) {
   v4i lo = *(const v4i*)p, hi = *(const v4i*)(p + 16);
@@ -82,23 +83,69 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
   static_assert(KS % KC == 0, "KS must split into equal chunks");
 
   extern __shared__ __align__(16) uint8_t smem[];
+  const int E = p.num_experts;
   uint8_t* sA = smem;                      // [RC][LDA] e4m3fn rows
   float* sAs = (float*)(sA + RC * LDA);    // [KS][RC] row scales (transposed)
   int* sSlot = (int*)(sAs + KS * RC);      // [RC] slot id of each staged row
   int* sAct = sSlot + RC;                  // [E] active experts, ascending
+  int* sCnt = sAct + E;                    // [E] slots per expert
+  int* sOff = sCnt + E;                    // [E] first slot-list entry per expert
+  int* sList = sOff + E;                   // [numel] slots grouped by expert (ids mode)
   __shared__ int sNact;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
-  const int E = p.num_experts;
+  const bool ids_mode = p.topk_ids != nullptr;
 
-  // ---- active experts (ascending), from the align kernel's counts
+  // ---- per-expert slot lists.  ids mode: built here from topk_ids (the
+  // order of slots inside an expert is irrelevant: every slot's outputs are
+  // computed independently).  Otherwise: the align kernel's offsets, counts
+  // and sorted_ids.
+  if (ids_mode) {
+    for (int e = tid; e < E; e += 256) sCnt[e] = 0;
+    __syncthreads();
+    int my_e[kStreamSlotsPerThread], my_pos[kStreamSlotsPerThread];
+#pragma unroll
+    for (int j = 0; j < kStreamSlotsPerThread; ++j) {
+      const int i = tid + j * 256;
+      int e = -1;
+      if (i < p.M) {
+        const int64_t v = p.ids_dtype == kI64 ? ((const int64_t*)p.topk_ids)[i]
+                                              : (int64_t)((const int32_t*)p.topk_ids)[i];
+        e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are skipped (.cu:44-46)
+      }
+      my_e[j] = e;
+      my_pos[j] = e >= 0 ? atomicAdd(&sCnt[e], 1) : 0;
+    }
+    __syncthreads();
+    if (w == 0) {
+      int run = 0;
+      for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const int c = e < E ? sCnt[e] : 0;
+        const int incl = wave_incl_scan(c);
+        if (e < E) sOff[e] = run + incl - c;
+        run += __shfl(incl, 63, 64);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kStreamSlotsPerThread; ++j)
+      if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * 256;
+  } else {
+    for (int e = tid; e < E; e += 256) {
+      sCnt[e] = p.expert_cnt[e];
+      sOff[e] = p.expert_off[e];
+    }
+  }
+  __syncthreads();
+  // ---- active experts, ascending
   if (w == 0) {
     int n = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
       const int e = e0 + lane;
-      const bool act = e < E && p.expert_cnt[e] > 0;
+      const bool act = e < E && sCnt[e] > 0;
       const uint64_t b = __ballot(act);
       if (act) sAct[n + __builtin_popcountll(b & ((1ull << lane) - 1ull))] = e;
       n += __builtin_popcountll(b);
@@ -119,8 +166,8 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
 
   for (int a = i0 / IPE; a * IPE < i1; ++a) {
     const int e = sAct[a];
-    const int cnt = p.expert_cnt[e];
-    const int off = p.expert_off[e];
+    const int cnt = sCnt[e];
+    const int off = sOff[e];
     const int ia0 = i0 > a * IPE ? i0 : a * IPE;
     const int ia1 = i1 < (a + 1) * IPE ? i1 : (a + 1) * IPE;
     const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride;
@@ -136,7 +183,7 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
         const bool live = gq < groups;
         const int rr = live ? gq / KS : 0, kk = live ? gq % KS : 0;
         int slot = 0;
-        if (live) slot = p.sorted_ids[off + r0 + rr];
+        if (live) slot = ids_mode ? sList[off + r0 + rr] : p.sorted_ids[off + r0 + rr];
         const int arow = slot / p.top_k;
         v4i raw = live ? *(const v4i*)(A16 + (int64_t)arow * p.lda + kk * 128 + sub * 8)
                        : v4i{0, 0, 0, 0};
@@ -244,7 +291,8 @@ template <int EPI, int KS, bool EXACT>
 static int run_stream_fp8(const GemmArgs& a, hipStream_t stream) {
   constexpr int K = KS * 128;
   const size_t shmem = (size_t)kStreamRows * (K + 16) + (size_t)KS * kStreamRows * 4 +
-                       kStreamRows * 4 + (size_t)a.num_experts * 4;
+                       kStreamRows * 4 + (size_t)a.num_experts * 3 * 4 +
+                       (a.topk_ids ? (size_t)a.M * 4 : 0);
   auto kern = stream_fp8_kernel<EPI, KS, EXACT>;
   static size_t attr_bytes = 0;  // largest LDS size opted in so far
   if (shmem > attr_bytes) {
@@ -269,8 +317,9 @@ bool stream_fp8_supported(int K, int N, int inter, int epi) {
 }
 
 int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream) {
-  if (!stream_fp8_supported(a.K, a.N, a.inter, epi) || a.num_experts > 1024) {
-    set_last_error("stream_fp8: unsupported shape (K=%d N=%d)", a.K, a.N);
+  if (!stream_fp8_supported(a.K, a.N, a.inter, epi) || a.num_experts > 1024 ||
+      (a.topk_ids && a.M > kStreamMaxIdsSlots)) {
+    set_last_error("stream_fp8: unsupported shape (K=%d N=%d slots=%lld)", a.K, a.N, (long long)a.M);
     return kUnsupported;
   }
 #define MSTAR_SF8(KS)                                                                       \
