@@ -135,37 +135,32 @@ def n_hit(logits):
 
 
 def gate_up_kernel_timing(x, logits, weights, steps, warmup):
-    """Mean duration of the gate_up streaming GEMM alone, from HIP events
-    recorded on the stream the kernel is launched on."""
-    from mstar_amd import _lib, ops
+    """Mean duration of the layer's gate_up GEMM alone (the kernel the decode
+    layer runs: weight streaming driven by the router ids, activations
+    quantised by the routing launch), from HIP events recorded on the stream
+    the kernel is launched on."""
+    from mstar_amd import _lib
     lib = _lib.load()
     M = x.shape[0]
-    tw, ti = ops.topk_softmax(logits, K_TOP, True)
-    slots = M * K_TOP
-    bm = 16
-    max_padded = slots + E * (bm - 1)
-    max_blocks = -(-max_padded // bm)
     dev = x.device
-    sorted_ids = torch.empty(max_padded, dtype=torch.int32, device=dev)
-    eids = torch.empty(max_blocks, dtype=torch.int32, device=dev)
-    ntpp = torch.empty(1, dtype=torch.int32, device=dev)
-    eoff = torch.empty(E + 1, dtype=torch.int32, device=dev)
-    ecnt = torch.empty(E, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
-    _lib.check(lib.mstar_moe_align_block_size(ti.data_ptr(), _lib.DT_I64, slots, E, bm,
-                                              sorted_ids.data_ptr(), max_padded, eids.data_ptr(),
-                                              max_blocks, ntpp.data_ptr(), eoff.data_ptr(),
-                                              ecnt.data_ptr(), None, 0, sp), "align")
+    tw = torch.empty(M, K_TOP, dtype=torch.float32, device=dev)
+    ti = torch.empty(M, K_TOP, dtype=torch.int32, device=dev)
+    hq = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    hs = torch.empty(M, H // 128, dtype=torch.float32, device=dev)
+    _lib.check(lib.mstar_moe_topk_softmax_quant(
+        logits.data_ptr(), _lib.DT_F32, M, E, K_TOP, 1, tw.data_ptr(), ti.data_ptr(), None,
+        x.data_ptr(), H, hq.data_ptr(), hs.data_ptr(), sp), "topk_softmax_quant")
+    slots = M * K_TOP
     c2 = torch.empty(slots, INTER, dtype=torch.bfloat16, device=dev)
 
     def launch(w):
         q1, s1, _, _ = w
-        _lib.check(lib.mstar_moe_gemm(
-            x.data_ptr(), _lib.DT_BF16, None, q1.data_ptr(), _lib.QUANT_FP8_W8A8, s1.data_ptr(),
-            c2.data_ptr(), _lib.DT_BF16, tw.data_ptr(), _lib.DT_F32, sorted_ids.data_ptr(),
-            eids.data_ptr(), ntpp.data_ptr(), eoff.data_ptr(), ecnt.data_ptr(), E, 2 * INTER, H,
-            max_padded, slots, K_TOP, 0, 0, bm, 2, sp), "moe_gemm")
+        _lib.check(lib.mstar_moe_stream_gemm(
+            hq.data_ptr(), _lib.DT_FP8_AS_BF16, hs.data_ptr(), q1.data_ptr(), s1.data_ptr(),
+            c2.data_ptr(), tw.data_ptr(), _lib.DT_F32, ti.data_ptr(), _lib.DT_I32, slots, E,
+            2 * INTER, H, K_TOP, 0, 0, sp), "moe_stream_gemm")
 
     for i in range(warmup):
         launch(weights[i % len(weights)])
@@ -272,7 +267,7 @@ def main():
                    "hit_experts": hits, "weight_copies_rotated": W_COPIES},
         "layer": {"us": round(us, 2), "algorithmic_bytes": layer_bytes, "GBps": round(layer_gbs, 1),
                   "hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
-        "roofline": {"kernel": "stream_fp8_kernel<EPI_ACT> (gate_up + SiLU-and-mul)", "bound": "hbm",
+        "roofline": {"kernel": "stream_fp8_cu_kernel<EPI_ACT> (gate_up + SiLU-and-mul)", "bound": "hbm",
                      "achieved": round(g1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g1_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic if M == 32 else None,

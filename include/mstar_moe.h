@@ -39,6 +39,9 @@ extern "C" {
 #define MSTAR_DTYPE_I32 3
 #define MSTAR_DTYPE_I64 4
 #define MSTAR_DTYPE_FP8_E4M3FN 5
+/* e4m3fn values stored widened to bf16 (exact: e4m3fn is a subset of bf16);
+ * the activation format the decode weight-streaming GEMM reads fastest. */
+#define MSTAR_DTYPE_FP8_AS_BF16 6
 
 /* quantisation modes of mstar_fused_moe */
 #define MSTAR_QUANT_NONE 0     /* w1/w2 in the activation dtype (bf16/fp16)          */
@@ -61,6 +64,20 @@ int mstar_moe_abi_version(void);
 int mstar_moe_topk_softmax(const void* logits, int logits_dtype, int64_t num_tokens,
                            int num_experts, int top_k, int renormalize, float* topk_weights,
                            int32_t* topk_ids_i32, int64_t* topk_ids_i64, void* stream);
+
+/* mstar_moe_topk_softmax plus the per-token-group-128 FP8 quantisation of
+ * the same tokens' hidden rows, in one launch (one wave per token): hidden
+ * [num_tokens, hidden_size] bf16 -> hidden_q [num_tokens, hidden_size]
+ * (MSTAR_DTYPE_FP8_AS_BF16: the e4m3fn values widened to bf16) and
+ * hidden_scale [num_tokens, hidden_size/128] fp32 (s = max(amax, 1e-10)/448).
+ * The routing step of the decode layer (moe.py:131-139) fused with the
+ * activation quantisation of the stripped FP8 path (kernels.py:3-7).
+ * hidden_size % 512 == 0. */
+int mstar_moe_topk_softmax_quant(const void* logits, int logits_dtype, int64_t num_tokens,
+                                 int num_experts, int top_k, int renormalize,
+                                 float* topk_weights, int32_t* topk_ids_i32,
+                                 int64_t* topk_ids_i64, const void* hidden, int64_t hidden_size,
+                                 void* hidden_q, float* hidden_scale, void* stream);
 
 /* Token permutation into expert-aligned blocks.
  * Replaces torch.ops._mstar_moe_C.moe_align_block_size
@@ -149,6 +166,25 @@ int mstar_moe_gemm(const void* A, int a_dtype, const float* a_scale, const void*
                    const int32_t* expert_counts, int num_experts, int64_t N, int64_t K,
                    int64_t em, int64_t num_valid_tokens, int top_k, int mul_routed_weight,
                    int activation, int block_size, int path, void* stream);
+
+/* Decode-sized FP8 grouped GEMM driven directly by the router ids: no
+ * alignment step.  The fused_moe_kernel of the reference
+ * (mstar/utils/fused_moe/kernels.py:36-138, launched by runner.py:118-152)
+ * for the fp8_w8a8 branch it stripped (kernels.py:3-7), as a weight stream:
+ * each hit expert's weights are read once.
+ *   topk_ids [num_slots] int32/int64 (slot s = token s / top_k);
+ *   A: a_dtype BF16 [rows, K] (quantised per group of 128 inside), or
+ *      FP8_AS_BF16 [rows, K] with a_scale [rows, K/128] (as written by
+ *      mstar_moe_topk_softmax_quant); A row of slot s = s / top_k;
+ *   B [E, N, K] e4m3fn, b_scale fp32 [E, ceil(N/128), K/128];
+ *   activation -1: C[s, :N] = bf16(acc (* topk_weights[s] if mul_routed));
+ *   activation 0/1: B rows [gate; up], C[s, :N/2] = act_and_mul.
+ * num_slots <= 1024, K % 128 == 0 with K/128 in {1,2,3,4,6,8,12,16}. */
+int mstar_moe_stream_gemm(const void* A, int a_dtype, const float* a_scale, const void* B,
+                          const float* b_scale, void* C, const void* topk_weights,
+                          int topk_w_dtype, const void* topk_ids, int ids_dtype,
+                          int64_t num_slots, int num_experts, int64_t N, int64_t K, int top_k,
+                          int mul_routed_weight, int activation, void* stream);
 
 /* Workspace bytes mstar_fused_moe needs for these sizes. */
 int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,

@@ -14,7 +14,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmstar_moe.so")
 
 # dtype codes (MSTAR_DTYPE_*)
-DT_F32, DT_BF16, DT_F16, DT_I32, DT_I64, DT_FP8 = 0, 1, 2, 3, 4, 5
+DT_F32, DT_BF16, DT_F16, DT_I32, DT_I64, DT_FP8, DT_FP8_AS_BF16 = 0, 1, 2, 3, 4, 5, 6
 QUANT_NONE, QUANT_FP8_W8A8, QUANT_W4A16 = 0, 1, 2
 
 _TORCH_DT = {
@@ -37,6 +37,9 @@ SIGNATURES = {
     "mstar_moe_last_error": (ctypes.c_char_p, []),
     "mstar_moe_abi_version": (_c_int, []),
     "mstar_moe_topk_softmax": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
+    "mstar_moe_topk_softmax_quant": (
+        _c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp,
+                 _vp]),
     "mstar_moe_align_block_size": (
         _c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _vp,
                  ctypes.c_size_t, _vp]),
@@ -54,6 +57,9 @@ SIGNATURES = {
         _c_int, [_vp, _c_int, _vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _vp,
                  _vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                  _c_int, _vp]),
+    "mstar_moe_stream_gemm": (
+        _c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_i64, _c_int, _c_i64,
+                 _c_i64, _c_int, _c_int, _c_int, _vp]),
     "mstar_fused_moe_workspace_size": (
         _c_int, [_c_i64, _c_i64, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int,
                  ctypes.POINTER(ctypes.c_size_t)]),

@@ -54,6 +54,9 @@ struct Plan {
   // FP8 weight streaming with the slot lists built inside the GEMMs from the
   // router ids: no alignment launch.
   bool ids_mode = false;
+  // The routing launch also quantises the hidden rows (hq/hs in the
+  // workspace) for the streaming gate_up GEMM.
+  bool route_quant = false;
   int bm = 16;
   int64_t slots = 0, max_padded = 0, max_blocks = 0;
   size_t off_sorted, off_eids, off_ntpp, off_eoff, off_ecnt, off_c2, off_c3, off_hq, off_hs,
@@ -101,8 +104,10 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->off_c2 = take((size_t)pl->slots * I * 2);
   pl->off_c3 = reduce ? take((size_t)pl->slots * H * 2) : 0;
   const bool fp8_tiled = quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream;
-  pl->off_hq = fp8_tiled ? take((size_t)M * H) : 0;
-  pl->off_hs = fp8_tiled ? take((size_t)M * (H / 128) * 4) : 0;
+  pl->route_quant = with_route && pl->ids_mode && H % 512 == 0 &&
+                    stream_fp8_tokens_fit(M, (int)H, E, pl->slots);
+  pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;
+  pl->off_hs = fp8_tiled || pl->route_quant ? take((size_t)M * (H / 128) * 4) : 0;
   pl->off_cq = fp8_tiled ? take((size_t)pl->slots * I) : 0;
   pl->off_cs = fp8_tiled ? take((size_t)pl->slots * (I / 128) * 4) : 0;
   pl->scratch_bytes = with_route ? route_scratch_bytes(M, top_k, E) : align_scratch_bytes(pl->slots, E);
@@ -179,6 +184,11 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
 
   if (pl.stream) {
     g1.A = hidden; g1.lda = H;
+    if (pl.route_quant) {
+      // The routing launch wrote the quantised hidden rows, widened to bf16.
+      g1.A = ws + pl.off_hq; g1.a_scale = (const float*)(ws + pl.off_hs); g1.ld_as = H / 128;
+      g1.a_q16 = 1;
+    }
     st = launch_stream_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, (int)M, stream);
     if (st != kOk) return st;
     st = launch_stream_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, (int)M, stream);
@@ -225,6 +235,59 @@ int mstar_moe_topk_softmax(const void* logits, int logits_dtype, int64_t num_tok
                            int32_t* topk_ids_i32, int64_t* topk_ids_i64, void* stream) {
   return launch_topk_softmax(logits, logits_dtype, num_tokens, num_experts, top_k, renormalize,
                              topk_weights, topk_ids_i32, topk_ids_i64, (hipStream_t)stream);
+}
+
+int mstar_moe_topk_softmax_quant(const void* logits, int logits_dtype, int64_t num_tokens,
+                                 int num_experts, int top_k, int renormalize,
+                                 float* topk_weights, int32_t* topk_ids_i32,
+                                 int64_t* topk_ids_i64, const void* hidden, int64_t hidden_size,
+                                 void* hidden_q, float* hidden_scale, void* stream) {
+  if (!hidden || !hidden_q || !hidden_scale) {
+    set_last_error("topk_softmax_quant: null hidden / hidden_q / hidden_scale");
+    return kInvalidArgument;
+  }
+  return launch_topk_softmax(logits, logits_dtype, num_tokens, num_experts, top_k, renormalize,
+                             topk_weights, topk_ids_i32, topk_ids_i64, (hipStream_t)stream,
+                             hidden, hidden_size, (uint16_t*)hidden_q, hidden_scale);
+}
+
+int mstar_moe_stream_gemm(const void* A, int a_dtype, const float* a_scale, const void* B,
+                          const float* b_scale, void* C, const void* topk_weights,
+                          int topk_w_dtype, const void* topk_ids, int ids_dtype,
+                          int64_t num_slots, int num_experts, int64_t N, int64_t K, int top_k,
+                          int mul_routed_weight, int activation, void* stream) {
+  if (num_slots < 0 || num_slots > kStreamMaxIdsSlots || num_experts <= 0 || N <= 0 || K <= 0 ||
+      top_k <= 0 || activation < -1 || activation > 1 || (activation >= 0 && N % 2 != 0)) {
+    set_last_error("moe_stream_gemm: invalid sizes (slots=%lld E=%d N=%lld K=%lld top_k=%d)",
+                   (long long)num_slots, num_experts, (long long)N, (long long)K, top_k);
+    return kInvalidArgument;
+  }
+  if (a_dtype != kBF16 && a_dtype != MSTAR_DTYPE_FP8_AS_BF16) {
+    set_last_error("moe_stream_gemm: A must be bf16 or FP8_AS_BF16");
+    return kUnsupported;
+  }
+  if (ids_dtype != kI32 && ids_dtype != kI64) {
+    set_last_error("moe_stream_gemm: topk_ids must be int32 or int64");
+    return kUnsupported;
+  }
+  if (num_slots == 0) return kOk;
+  if (!A || !B || !b_scale || !C || !topk_ids || (a_dtype != kBF16 && !a_scale) ||
+      (mul_routed_weight && !topk_weights)) {
+    set_last_error("moe_stream_gemm: null tensor pointer");
+    return kInvalidArgument;
+  }
+  GemmArgs g = {};
+  g.A = A; g.lda = K;
+  if (a_dtype != kBF16) { g.a_scale = a_scale; g.ld_as = K / 128; g.a_q16 = 1; }
+  g.B = B; g.ldb = K; g.b_estride = N * K; g.b_scale = b_scale;
+  g.bs_ld = K / 128; g.bs_estride = ((N + 127) / 128) * (K / 128);
+  g.C = C; g.ldc = activation >= 0 ? N / 2 : N;
+  g.topk_w = topk_weights; g.topk_w_dtype = topk_w_dtype;
+  g.topk_ids = topk_ids; g.ids_dtype = ids_dtype;
+  g.M = num_slots; g.N = (int)N; g.K = (int)K; g.top_k = top_k; g.inter = (int)(N / 2);
+  g.mul_routed = mul_routed_weight; g.activation = activation < 0 ? 0 : activation;
+  g.num_experts = num_experts;
+  return launch_stream_fp8(g, activation >= 0 ? EPI_ACT : EPI_STORE, true, (hipStream_t)stream);
 }
 
 int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
@@ -454,7 +517,9 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
   int32_t* ids32 = (int32_t*)(ws + pl.off_ids);
   if (pl.ids_mode)
     st = launch_topk_softmax(router_logits, logits_dtype, num_tokens, num_experts, top_k,
-                             renormalize, tw, ids32, topk_ids_out, stream);
+                             renormalize, tw, ids32, topk_ids_out, stream,
+                             pl.route_quant ? hidden : nullptr, hidden_size,
+                             (uint16_t*)(ws + pl.off_hq), (float*)(ws + pl.off_hs));
   else
     st = launch_route(router_logits, logits_dtype, num_tokens, num_experts, top_k, renormalize, tw,
                       ids32, topk_ids_out, pl.bm, (int32_t*)(ws + pl.off_sorted),

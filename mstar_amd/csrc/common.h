@@ -103,6 +103,51 @@ __device__ inline float group_max(float v) {
   return v;
 }
 
+// Eight e4m3fn codes (two dwords) widened exactly to eight bf16 (e4m3fn is a
+// subset of bf16).  Whole 32-bit pairs are moved: extracting single __bf16
+// elements from the packed results makes the compiler insert byte permutes
+// that scramble the pairs.
+__device__ __forceinline__ v4i fp8x8_to_bf16x8_bits(int x0, int x1) {
+  const int c0 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x0, 1.0f, false));
+  const int c1 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x0, 1.0f, true));
+  const int c2 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x1, 1.0f, false));
+  const int c3 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x1, 1.0f, true));
+  return v4i{c0, c1, c2, c3};
+}
+
+// Raw buffer resource over [base, base + bytes): buffer loads at offsets
+// >= bytes return zeros without a memory request, which is how lanes with
+// nothing to load are masked without a branch.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t kOffNone = 0xFFFFFFF0u;  // an offset no buffer here reaches
+
+// Per-token-group-128 FP8 quantisation of 8 consecutive 16-bit elements
+// (raw: 16 bytes of bf16/fp16 bits); the 16 aligned lanes that hold one
+// 128-element group cooperate on its amax.  s = max(amax, 1e-10) / 448 and
+// q = e4m3fn(clamp(x / s)) with IEEE division and round-to-nearest-even, so
+// the codes equal a CPU restatement bit for bit.  Returns the 8 codes.
+template <int DT>
+__device__ __forceinline__ int2 quant_group8(v4i raw, float& scale) {
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = h16_to_f32<DT>((uint16_t)(raw[i] & 0xffff));
+    f[2 * i + 1] = h16_to_f32<DT>((uint16_t)((uint32_t)raw[i] >> 16));
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  amax = group_max<16>(amax);
+  const float sc = fmaxf(amax, kQuantEps) / kFp8Max;
+  scale = sc;
+  return make_int2(cvt_fp8x4(clamp_fp8(f[0] / sc), clamp_fp8(f[1] / sc), clamp_fp8(f[2] / sc),
+                             clamp_fp8(f[3] / sc)),
+                   cvt_fp8x4(clamp_fp8(f[4] / sc), clamp_fp8(f[5] / sc), clamp_fp8(f[6] / sc),
+                             clamp_fp8(f[7] / sc)));
+}
+
 // Inclusive prefix sum across the 64 lanes of a wave.
 __device__ inline int wave_incl_scan(int v) {
   const int l = lane_id();

@@ -9,8 +9,13 @@
 namespace mstar {
 
 // route.hip
+// With `hidden` (bf16 [M, H], H % 512 == 0) the launch also quantises the
+// hidden rows per group of 128: hq [M, H] holds the e4m3fn values widened to
+// bf16, hs [M, H/128] the scales.
 int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, int k,
-                        int renorm, float* w, int32_t* ids32, int64_t* ids64, hipStream_t stream);
+                        int renorm, float* w, int32_t* ids32, int64_t* ids64, hipStream_t stream,
+                        const void* hidden = nullptr, int64_t H = 0, uint16_t* hq = nullptr,
+                        float* hs = nullptr);
 // Alignment: one workgroup for numel <= 4096 (or without scratch), otherwise
 // a histogram pass and a scan+scatter pass over align_scratch_bytes() of
 // scratch.  Deterministic (slots ascend within an expert) either way.
@@ -29,8 +34,9 @@ int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, 
 size_t route_scratch_bytes(int64_t M, int k, int E);
 
 // quant.hip
+// widen: q receives the e4m3fn values widened to bf16 (2 bytes per element).
 int launch_quant_fp8_group(const void* x, int x_dtype, int64_t rows, int64_t cols,
-                           int64_t ld_x, uint8_t* q, float* s, hipStream_t stream);
+                           int64_t ld_x, void* q, float* s, hipStream_t stream, bool widen = false);
 int launch_quant_fp8_row(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q,
                          float* s, hipStream_t stream);
 
@@ -82,6 +88,9 @@ struct GemmArgs {
   // sorted_ids / expert_off / expert_cnt.
   const void* topk_ids;
   int ids_dtype;
+  // A_FP8G rows hold the e4m3fn values widened to bf16 (2 bytes per
+  // element, lda in elements) instead of e4m3fn bytes.
+  int a_q16;
 };
 
 // Tiled grouped / dense GEMM (LDS-staged MFMA tiles); bm is the row block.
@@ -106,5 +115,9 @@ constexpr int kBigBlockM = 256;
 int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream);
 constexpr int64_t kStreamMaxIdsSlots = 1024;  // slots a launch in ids mode can take
 bool stream_fp8_supported(int K, int N, int inter, int epi);
+// Whether `tokens` activation rows of K values, widened to bf16, fit the LDS
+// of the CU-resident streaming kernel (the condition for feeding it
+// pre-quantised widened rows).
+bool stream_fp8_tokens_fit(int64_t tokens, int K, int E, int64_t slots);
 
 }  // namespace mstar

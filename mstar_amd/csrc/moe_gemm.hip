@@ -626,7 +626,8 @@ int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dty
                    bkind, dtype);
     return kUnsupported;
   }
-  if (!a.expert_off || !a.expert_cnt || !a.sorted_ids || (epi == EPI_ACT && a.N != 2 * a.inter)) {
+  if ((!a.topk_ids && (!a.expert_off || !a.expert_cnt || !a.sorted_ids)) ||
+      (epi == EPI_ACT && a.N != 2 * a.inter)) {
     set_last_error("stream_gemm: missing expert offsets/counts or bad shapes");
     return kInvalidArgument;
   }

@@ -12,11 +12,11 @@
 namespace mstar {
 
 // 16 lanes per 128-element group, 8 elements per lane.
-template <int DT>
+// WIDEN: q holds the e4m3fn values widened to bf16 (2 bytes per element).
+template <int DT, bool WIDEN>
 __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __restrict__ x,
                                                               int64_t rows, int64_t cols,
-                                                              int64_t ld_x,
-                                                              uint8_t* __restrict__ q,
+                                                              int64_t ld_x, void* __restrict__ q,
                                                               float* __restrict__ s) {
   const int64_t gpr = cols / 128;
   const int64_t g = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 16;
@@ -24,23 +24,13 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __
   const bool live = g < rows * gpr;
   const int64_t r = live ? g / gpr : 0, c = live ? (g % gpr) * 128 + sub * 8 : 0;
   v4i raw = live ? *(const v4i*)(x + r * ld_x + c) : v4i{0, 0, 0, 0};
-  float f[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = h16_to_f32<DT>((uint16_t)(raw[i] & 0xffff));
-    f[2 * i + 1] = h16_to_f32<DT>((uint16_t)((uint32_t)raw[i] >> 16));
-  }
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-  amax = group_max<16>(amax);
-  const float sc = fmaxf(amax, kQuantEps) / kFp8Max;
-  const int lo = cvt_fp8x4(clamp_fp8(f[0] / sc), clamp_fp8(f[1] / sc), clamp_fp8(f[2] / sc),
-                           clamp_fp8(f[3] / sc));
-  const int hi = cvt_fp8x4(clamp_fp8(f[4] / sc), clamp_fp8(f[5] / sc), clamp_fp8(f[6] / sc),
-                           clamp_fp8(f[7] / sc));
+  float sc;
+  const int2 codes = quant_group8<DT>(raw, sc);
   if (live) {
-    *(int2*)(q + r * cols + c) = make_int2(lo, hi);
+    if constexpr (WIDEN)
+      *(v4i*)((uint16_t*)q + r * cols + c) = fp8x8_to_bf16x8_bits(codes.x, codes.y);
+    else
+      *(int2*)((uint8_t*)q + r * cols + c) = codes;
     if (sub == 0) s[r * gpr + c / 128] = sc;
   }
 }
@@ -69,7 +59,7 @@ __global__ __launch_bounds__(256) void quant_fp8_row_kernel(const uint16_t* __re
 }
 
 int launch_quant_fp8_group(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld_x,
-                           uint8_t* q, float* s, hipStream_t stream) {
+                           void* q, float* s, hipStream_t stream, bool widen) {
   if (rows < 0 || cols <= 0 || cols % 128 != 0 || ld_x < cols || ld_x % 8 != 0) {
     set_last_error("quant_fp8_group: cols must be a positive multiple of 128 (cols=%lld)",
                    (long long)cols);
@@ -79,9 +69,11 @@ int launch_quant_fp8_group(const void* x, int x_dtype, int64_t rows, int64_t col
   const int64_t groups = rows * (cols / 128);
   dim3 grid((unsigned)((groups * 16 + 255) / 256));
   if (x_dtype == kBF16)
-    quant_fp8_group_kernel<kBF16><<<grid, 256, 0, stream>>>((const uint16_t*)x, rows, cols, ld_x, q, s);
+    widen ? quant_fp8_group_kernel<kBF16, true><<<grid, 256, 0, stream>>>((const uint16_t*)x, rows, cols, ld_x, q, s)
+          : quant_fp8_group_kernel<kBF16, false><<<grid, 256, 0, stream>>>((const uint16_t*)x, rows, cols, ld_x, q, s);
   else if (x_dtype == kF16)
-    quant_fp8_group_kernel<kF16><<<grid, 256, 0, stream>>>((const uint16_t*)x, rows, cols, ld_x, q, s);
+    widen ? quant_fp8_group_kernel<kF16, true><<<grid, 256, 0, stream>>>((const uint16_t*)x, rows, cols, ld_x, q, s)
+          : quant_fp8_group_kernel<kF16, false><<<grid, 256, 0, stream>>>((const uint16_t*)x, rows, cols, ld_x, q, s);
   else {
     set_last_error("quant_fp8_group: input must be bf16 or fp16");
     return kUnsupported;

@@ -149,12 +149,19 @@ __device__ __forceinline__ void topk_tokens(const LT* __restrict__ logits, int64
   }
 }
 
+// One wave per token.  With `hidden`, the wave also quantises the token's
+// bf16 hidden row per group of 128 for the FP8 expert GEMMs that follow (hq
+// [M, H]: the e4m3fn values widened to bf16; hs [M, H/128]): the routing
+// launch carries the activation quantisation for free.
 template <typename LT, int EPL>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict__ logits,
                                                            int64_t M, int E, int k, int renorm,
                                                            float* __restrict__ w_out,
                                                            int32_t* __restrict__ ids32,
-                                                           int64_t* __restrict__ ids64) {
+                                                           int64_t* __restrict__ ids64,
+                                                           const uint16_t* __restrict__ hidden,
+                                                           int64_t H, uint16_t* __restrict__ hq,
+                                                           float* __restrict__ hs) {
   const int lane = threadIdx.x & 63;
   const int64_t tok = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (tok >= M) return;
@@ -164,11 +171,39 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict_
     const int e = j * 64 + lane;
     v[j] = e < E ? load_logit<LT>(logits + tok * E, e) : -INFINITY;
   }
+  // Hidden row loads go out with the logits (4 groups of 128 per pass).
+  constexpr int kQB = 4;
+  v4i raw[kQB];
+  if (hidden) {
+#pragma unroll
+    for (int b = 0; b < kQB; ++b) {
+      const int64_t c = (int64_t)b * 512 + lane * 8;
+      raw[b] = c < H ? *(const v4i*)(hidden + tok * H + c) : v4i{0, 0, 0, 0};
+    }
+  }
   topk_wave<EPL>(v, E, k, renorm, lane, [&](int r, int id, float w) {
     w_out[tok * k + r] = w;
     if (ids32) ids32[tok * k + r] = id;
     if (ids64) ids64[tok * k + r] = id;
   });
+  if (!hidden) return;
+  for (int64_t c0 = 0; c0 < H; c0 += kQB * 512) {
+#pragma unroll
+    for (int b = 0; b < kQB; ++b) {
+      const int64_t c = c0 + (int64_t)b * 512 + lane * 8;
+      if (c0 > 0) raw[b] = c < H ? *(const v4i*)(hidden + tok * H + c) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int b = 0; b < kQB; ++b) {
+      const int64_t c = c0 + (int64_t)b * 512 + lane * 8;
+      float sc;
+      const int2 codes = quant_group8<kBF16>(raw[b], sc);
+      if (c < H) {
+        *(v4i*)(hq + tok * H + c) = fp8x8_to_bf16x8_bits(codes.x, codes.y);
+        if ((lane & 15) == 0) hs[tok * (H / 128) + c / 128] = sc;
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -472,7 +507,12 @@ __global__ __launch_bounds__(kAlignThreads) void scatter_kernel(
 // ---------------------------------------------------------------------------
 int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, int k,
                         int renorm, float* w, int32_t* ids32, int64_t* ids64,
-                        hipStream_t stream) {
+                        hipStream_t stream, const void* hidden, int64_t H, uint16_t* hq,
+                        float* hs) {
+  if (hidden && (H <= 0 || H % 512 != 0 || !hq || !hs)) {
+    set_last_error("topk_softmax: hidden quantisation needs H %% 512 == 0 (H=%lld)", (long long)H);
+    return kInvalidArgument;
+  }
   if (M < 0 || E <= 0 || E > 1024 || k <= 0 || k > 64 || k > E || !w || (!ids32 && !ids64) ||
       (M > 0 && !logits)) {
     set_last_error("topk_softmax: invalid arguments (M=%lld E=%d k=%d)", (long long)M, E, k);
@@ -492,41 +532,22 @@ int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, 
 #define MSTAR_TOPK_CASE(N)                                                                   \
   case N:                                                                                    \
     if (logits_dtype == kF32)                                                                \
-      topk_softmax_kernel<float, N><<<grid, block, 0, stream>>>((const float*)logits, M, E, \
-                                                                k, renorm, w, ids32, ids64); \
+      topk_softmax_kernel<float, N><<<grid, block, 0, stream>>>(                             \
+          (const float*)logits, M, E, k, renorm, w, ids32, ids64, (const uint16_t*)hidden, H, \
+          hq, hs);                                                                           \
     else                                                                                     \
       topk_softmax_kernel<uint16_t, N><<<grid, block, 0, stream>>>(                          \
-          (const uint16_t*)logits, M, E, k, renorm, w, ids32, ids64);                        \
+          (const uint16_t*)logits, M, E, k, renorm, w, ids32, ids64, (const uint16_t*)hidden, \
+          H, hq, hs);                                                                        \
     break;
-  switch (epl) {
+  // Experts per lane, rounded up to a power of two (E <= 1024).
+  const int epl2 = epl <= 1 ? 1 : epl <= 2 ? 2 : epl <= 4 ? 4 : epl <= 8 ? 8 : 16;
+  switch (epl2) {
     MSTAR_TOPK_CASE(1)
     MSTAR_TOPK_CASE(2)
     MSTAR_TOPK_CASE(4)
     MSTAR_TOPK_CASE(8)
     MSTAR_TOPK_CASE(16)
-    default:
-      if (epl == 3) {
-        if (logits_dtype == kF32)
-          topk_softmax_kernel<float, 4><<<grid, block, 0, stream>>>((const float*)logits, M, E, k,
-                                                                   renorm, w, ids32, ids64);
-        else
-          topk_softmax_kernel<uint16_t, 4><<<grid, block, 0, stream>>>(
-              (const uint16_t*)logits, M, E, k, renorm, w, ids32, ids64);
-      } else if (epl <= 8) {
-        if (logits_dtype == kF32)
-          topk_softmax_kernel<float, 8><<<grid, block, 0, stream>>>((const float*)logits, M, E, k,
-                                                                   renorm, w, ids32, ids64);
-        else
-          topk_softmax_kernel<uint16_t, 8><<<grid, block, 0, stream>>>(
-              (const uint16_t*)logits, M, E, k, renorm, w, ids32, ids64);
-      } else {
-        if (logits_dtype == kF32)
-          topk_softmax_kernel<float, 16><<<grid, block, 0, stream>>>(
-              (const float*)logits, M, E, k, renorm, w, ids32, ids64);
-        else
-          topk_softmax_kernel<uint16_t, 16><<<grid, block, 0, stream>>>(
-              (const uint16_t*)logits, M, E, k, renorm, w, ids32, ids64);
-      }
   }
 #undef MSTAR_TOPK_CASE
   return launch_status("topk_softmax");

@@ -34,24 +34,16 @@ namespace mstar {
 constexpr int kStreamRows = 16;   // token rows staged per pass (one MFMA row block)
 constexpr int kStreamWaves = 4;   // waves per workgroup
 constexpr int kStreamWgPerCu = 4; // resident workgroups per CU (LDS ~35 KB each)
-constexpr int kStreamSlotsPerThread = 4;  // ids mode: up to 1024 slots per launch
+constexpr int kGatherBatchQ = 4;          // 16-byte row pieces in flight per thread (FP8 rows)
+constexpr int kGatherBatchH = 3;          // groups in flight per 16 lanes (bf16 rows)
 
 __device__ inline v8i lds_v8i(const uint8_t* p) {
   v4i lo = *(const v4i*)p, hi = *(const v4i*)(p + 16);
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Eight e4m3fn bytes (two dwords) -> one bf16x8 MFMA operand, exactly
-// (e4m3fn is a subset of bf16).  Whole 32-bit pairs are moved: pulling
-// single __bf16 elements out of the packed result makes the compiler insert
-// byte permutes that scramble the pairs.
 __device__ inline v8s fp8x8_to_bf16x8(int x0, int x1) {
-  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-  const int c0 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x0, 1.0f, false));
-  const int c1 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x0, 1.0f, true));
-  const int c2 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x1, 1.0f, false));
-  const int c3 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((unsigned)x1, 1.0f, true));
-  return __builtin_bit_cast(v8s, v4i{c0, c1, c2, c3});
+  return __builtin_bit_cast(v8s, fp8x8_to_bf16x8_bits(x0, x1));
 }
 
 // One 16x16x128 block product of e4m3fn fragments.  EXACT: the fragments
@@ -73,42 +65,28 @@ __device__ inline v4f block_dot_fp8(const v8i& a, const v8i& b) {
   }
 }
 
-template <int EPI, int KS, bool EXACT>
-__global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
-  constexpr int K = KS * 128;
-  constexpr int KC = KS <= 6 ? KS : (KS % 4 == 0 ? 4 : (KS % 3 == 0 ? 3 : KS));  // K steps loaded at once
-  constexpr int CH = KS / KC;                                   // loads per item
-  constexpr int LDA = K + 16;
-  constexpr int RC = kStreamRows;
-  static_assert(KS % KC == 0, "KS must split into equal chunks");
-
-  extern __shared__ __align__(16) uint8_t smem[];
+// Per-expert slot lists in LDS.  ids mode (p.topk_ids set): built from the
+// router ids (the order of slots inside an expert is irrelevant: every
+// slot's outputs are computed independently).  Otherwise: the align
+// kernel's offsets, counts and sorted_ids.  Then the active experts,
+// ascending, and their number.  Ends with a barrier.
+template <int NT>
+__device__ __forceinline__ void build_expert_lists(const GemmArgs& p, int tid, int w, int lane,
+                                                   int* sAct, int* sCnt, int* sOff, int* sList,
+                                                   int* nact) {
+  constexpr int SPT = (int)(kStreamMaxIdsSlots / NT);  // slots per thread
   const int E = p.num_experts;
-  uint8_t* sA = smem;                      // [RC][LDA] e4m3fn rows
-  float* sAs = (float*)(sA + RC * LDA);    // [KS][RC] row scales (transposed)
-  int* sSlot = (int*)(sAs + KS * RC);      // [RC] slot id of each staged row
-  int* sAct = sSlot + RC;                  // [E] active experts, ascending
-  int* sCnt = sAct + E;                    // [E] slots per expert
-  int* sOff = sCnt + E;                    // [E] first slot-list entry per expert
-  int* sList = sOff + E;                   // [numel] slots grouped by expert (ids mode)
-  __shared__ int sNact;
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l16 = lane & 15, lg = lane >> 4;
-  const bool ids_mode = p.topk_ids != nullptr;
-
   // ---- per-expert slot lists.  ids mode: built here from topk_ids (the
   // order of slots inside an expert is irrelevant: every slot's outputs are
   // computed independently).  Otherwise: the align kernel's offsets, counts
   // and sorted_ids.
-  if (ids_mode) {
-    for (int e = tid; e < E; e += 256) sCnt[e] = 0;
+  if (p.topk_ids) {
+    for (int e = tid; e < E; e += NT) sCnt[e] = 0;
     __syncthreads();
-    int my_e[kStreamSlotsPerThread], my_pos[kStreamSlotsPerThread];
+    int my_e[SPT], my_pos[SPT];
 #pragma unroll
-    for (int j = 0; j < kStreamSlotsPerThread; ++j) {
-      const int i = tid + j * 256;
+    for (int j = 0; j < SPT; ++j) {
+      const int i = tid + j * NT;
       int e = -1;
       if (i < p.M) {
         const int64_t v = p.ids_dtype == kI64 ? ((const int64_t*)p.topk_ids)[i]
@@ -131,10 +109,10 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kStreamSlotsPerThread; ++j)
-      if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * 256;
+    for (int j = 0; j < SPT; ++j)
+      if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * NT;
   } else {
-    for (int e = tid; e < E; e += 256) {
+    for (int e = tid; e < E; e += NT) {
       sCnt[e] = p.expert_cnt[e];
       sOff[e] = p.expert_off[e];
     }
@@ -150,9 +128,38 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
       if (act) sAct[n + __builtin_popcountll(b & ((1ull << lane) - 1ull))] = e;
       n += __builtin_popcountll(b);
     }
-    if (lane == 0) sNact = n;
+    if (lane == 0) *nact = n;
   }
   __syncthreads();
+}
+
+template <int EPI, int KS, bool EXACT, bool AQ>
+__global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
+  constexpr int K = KS * 128;
+  // K-steps per chunk; two chunks are in flight per wave.
+  constexpr int KC = KS % 2 == 0 ? 2 : (KS % 3 == 0 ? 3 : 1);
+  constexpr int CH = KS / KC;                                   // loads per item
+  constexpr int LDA = K + 16;
+  constexpr int RC = kStreamRows;
+  static_assert(KS % KC == 0, "KS must split into equal chunks");
+
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int E = p.num_experts;
+  uint8_t* sA = smem;                      // [RC][LDA] e4m3fn rows
+  float* sAs = (float*)(sA + RC * LDA);    // [KS][RC] row scales (transposed)
+  int* sSlot = (int*)(sAs + KS * RC);      // [RC] slot id of each staged row
+  int* sAct = sSlot + RC;                  // [E] active experts, ascending
+  int* sCnt = sAct + E;                    // [E] slots per expert
+  int* sOff = sCnt + E;                    // [E] first slot-list entry per expert
+  int* sList = sOff + E;                   // [numel] slots grouped by expert (ids mode)
+  __shared__ int sNact;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const bool ids_mode = p.topk_ids != nullptr;
+
+  build_expert_lists<256>(p, tid, w, lane, sAct, sCnt, sOff, sList, &sNact);
   const int n_act = sNact;
   const int IPE = EPI == EPI_ACT ? p.inter / 8 : p.N / 16;  // wave items per expert
   const int total = n_act * IPE;
@@ -172,41 +179,105 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
     const int ia1 = i1 < (a + 1) * IPE ? i1 : (a + 1) * IPE;
     const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride;
     const float* Se = (const float*)p.b_scale + (int64_t)e * p.bs_estride;
+    // This wave's work in the expert: items ia0 + w, ia0 + w + 4, ...; each
+    // item is CH chunks of KC K-steps.  q enumerates (item, chunk) pairs.
+    const int my_items = ia0 + w < ia1 ? (ia1 - ia0 - w + kStreamWaves - 1) / kStreamWaves : 0;
+    const int nq = my_items * CH;
+
+    // Weight row of this lane for item `it`.
+    auto weight_row = [&](int it) -> int {
+      const int g = it - a * IPE;
+      if constexpr (EPI == EPI_ACT) {
+        const int ocol = g * 8 + (l16 & 7);
+        return l16 < 8 ? ocol : p.inter + ocol;
+      } else {
+        return g * 16 + l16;
+      }
+    };
+    // Loads of chunk q: KC weight fragments (32 bytes per lane and K-step)
+    // and their block scales.
+    auto load_chunk = [&](int q, v8i (&bq)[KC], float (&sq)[KC]) {
+      const int it = ia0 + w + (q / CH) * kStreamWaves, c = q % CH;
+      const int br = weight_row(it);
+      const uint8_t* src = Be + (int64_t)br * p.ldb + lg * 32 + c * KC * 128;
+      const float* ss = Se + (int64_t)(br / 128) * p.bs_ld + c * KC;
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+        bq[kk] = *(const v8i*)(src + kk * 128);
+        sq[kk] = ss[kk];
+      }
+    };
 
     for (int r0 = 0; r0 < cnt; r0 += RC) {
       const int rows = cnt - r0 < RC ? cnt - r0 : RC;
+      // Two register buffers: chunk q+1 is in flight while chunk q computes.
+      // The first chunk is issued before the token gather so its latency
+      // overlaps the gather and the barrier.
+      v8i b0[KC], b1[KC];
+      float s0[KC], s1[KC];
+      if (nq > 0) load_chunk(0, b0, s0);
       __syncthreads();  // the previous pass is done with LDS
-      // ---- gather + quantise the expert's token rows into LDS
-      const int groups = rows * KS;
-      for (int g0 = 0; g0 < groups; g0 += 16) {
-        const int gq = g0 + (tid >> 4), sub = tid & 15;
-        const bool live = gq < groups;
-        const int rr = live ? gq / KS : 0, kk = live ? gq % KS : 0;
-        int slot = 0;
-        if (live) slot = ids_mode ? sList[off + r0 + rr] : p.sorted_ids[off + r0 + rr];
-        const int arow = slot / p.top_k;
-        v4i raw = live ? *(const v4i*)(A16 + (int64_t)arow * p.lda + kk * 128 + sub * 8)
-                       : v4i{0, 0, 0, 0};
-        float f[8];
+      // ---- stage the expert's token rows (e4m3fn) and group scales in LDS.
+      // All loads of a batch are issued before any is used.
+      auto slot_of = [&](int rr) { return ids_mode ? sList[off + r0 + rr] : p.sorted_ids[off + r0 + rr]; };
+      if constexpr (AQ) {
+        // Pre-quantised rows: a copy.
+        constexpr int PPR = K / 16;  // 16-byte pieces per row
+        constexpr int B = kGatherBatchQ;
+        const int pieces = rows * PPR;
+        const uint8_t* A8 = (const uint8_t*)p.A;
+        for (int base = 0; base < pieces; base += 256 * B) {
+          v4i v[B];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f[2 * i] = bf16_bits_to_f32((uint16_t)(raw[i] & 0xffff));
-          f[2 * i + 1] = bf16_bits_to_f32((uint16_t)((uint32_t)raw[i] >> 16));
+          for (int j = 0; j < B; ++j) {
+            const int pc = base + j * 256 + tid;
+            const int rr = pc / PPR, c = pc % PPR;
+            v[j] = pc < pieces ? *(const v4i*)(A8 + (int64_t)(slot_of(rr) / p.top_k) * p.lda + c * 16)
+                               : v4i{0, 0, 0, 0};
+          }
+#pragma unroll
+          for (int j = 0; j < B; ++j) {
+            const int pc = base + j * 256 + tid;
+            const int rr = pc / PPR, c = pc % PPR;
+            if (pc < pieces) *(v4i*)(sA + rr * LDA + c * 16) = v[j];
+          }
         }
-        float amax = 0.f;
+        for (int i = tid; i < rows * KS; i += 256) {
+          const int rr = i / KS, kk = i % KS;
+          const int slot = slot_of(rr);
+          sAs[kk * RC + rr] = p.a_scale[(int64_t)(slot / p.top_k) * p.ld_as + kk];
+          if (kk == 0) sSlot[rr] = slot;
+        }
+      } else {
+        // bf16 rows, quantised per group of 128 here (16 lanes per group).
+        constexpr int B = kGatherBatchH;
+        const int groups = rows * KS;
+        for (int g0 = 0; g0 < groups; g0 += 16 * B) {
+          v4i raw[B];
+          int slots[B];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-        amax = group_max<16>(amax);
-        const float sc = fmaxf(amax, kQuantEps) / kFp8Max;
-        const int lo = cvt_fp8x4(clamp_fp8(f[0] / sc), clamp_fp8(f[1] / sc),
-                                 clamp_fp8(f[2] / sc), clamp_fp8(f[3] / sc));
-        const int hi = cvt_fp8x4(clamp_fp8(f[4] / sc), clamp_fp8(f[5] / sc),
-                                 clamp_fp8(f[6] / sc), clamp_fp8(f[7] / sc));
-        if (live) {
-          *(int2*)(sA + rr * LDA + kk * 128 + sub * 8) = make_int2(lo, hi);
-          if (sub == 0) {
-            sAs[kk * RC + rr] = sc;
-            if (kk == 0) sSlot[rr] = slot;
+          for (int j = 0; j < B; ++j) {
+            const int gq = g0 + j * 16 + (tid >> 4), sub = tid & 15;
+            const bool live = gq < groups;
+            const int rr = live ? gq / KS : 0, kk = live ? gq % KS : 0;
+            slots[j] = live ? slot_of(rr) : 0;
+            raw[j] = live ? *(const v4i*)(A16 + (int64_t)(slots[j] / p.top_k) * p.lda + kk * 128 + sub * 8)
+                          : v4i{0, 0, 0, 0};
+          }
+#pragma unroll
+          for (int j = 0; j < B; ++j) {
+            const int gq = g0 + j * 16 + (tid >> 4), sub = tid & 15;
+            const bool live = gq < groups;
+            const int rr = live ? gq / KS : 0, kk = live ? gq % KS : 0;
+            float sc;
+            const int2 codes = quant_group8<kBF16>(raw[j], sc);
+            if (live) {
+              *(int2*)(sA + rr * LDA + kk * 128 + sub * 8) = codes;
+              if (sub == 0) {
+                sAs[kk * RC + rr] = sc;
+                if (kk == 0) sSlot[rr] = slots[j];
+              }
+            }
           }
         }
       }
@@ -216,38 +287,22 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
       __syncthreads();
 
       const bool arow_ok = l16 < rows;
-      for (int it = ia0 + w; it < ia1; it += kStreamWaves) {
+      v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+      // Chunk q: MFMAs of its KC K-steps; after an item's last chunk, the
+      // item's epilogue.
+      auto compute = [&](int q, const v8i (&bq)[KC], const float (&sq)[KC]) {
+        const int it = ia0 + w + (q / CH) * kStreamWaves, c = q % CH;
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk) {
+          const int kg = c * KC + kk;
+          v8i af = arow_ok ? lds_v8i(sA + l16 * LDA + kg * 128 + lg * 32)
+                           : v8i{0, 0, 0, 0, 0, 0, 0, 0};
+          v4f t = block_dot_fp8<EXACT>(af, bq[kk]);
+          v4f sa = *(const v4f*)(sAs + kg * RC + lg * 4);
+          acc += t * (sa * sq[kk]);
+        }
+        if (c != CH - 1) return;
         const int g = it - a * IPE;
-        int br;
-        if constexpr (EPI == EPI_ACT) {
-          const int ocol = g * 8 + (l16 & 7);
-          br = l16 < 8 ? ocol : p.inter + ocol;
-        } else {
-          br = g * 16 + l16;
-        }
-        const uint8_t* src = Be + (int64_t)br * p.ldb + lg * 32;
-        const float* ss = Se + (int64_t)(br / 128) * p.bs_ld;
-        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-        for (int c = 0; c < CH; ++c) {
-          v8i b[KC];
-          float sw[KC];
-#pragma unroll
-          for (int kk = 0; kk < KC; ++kk) {
-            b[kk] = *(const v8i*)(src + (c * KC + kk) * 128);
-            sw[kk] = ss[c * KC + kk];
-          }
-#pragma unroll
-          for (int kk = 0; kk < KC; ++kk) {
-            const int kg = c * KC + kk;
-            v8i af = arow_ok ? lds_v8i(sA + l16 * LDA + kg * 128 + lg * 32)
-                             : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-            v4f t = block_dot_fp8<EXACT>(af, b[kk]);
-            v4f sa = *(const v4f*)(sAs + kg * RC + lg * 4);
-            acc += t * (sa * sw[kk]);
-          }
-        }
-        // ---- epilogue of item g
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int orow = lg * 4 + r;
@@ -269,7 +324,287 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
             }
           }
         }
+        acc = v4f{0.f, 0.f, 0.f, 0.f};
+      };
+#pragma unroll 1
+      for (int q = 0; q < nq; q += 2) {
+        if (q + 1 < nq) load_chunk(q + 1, b1, s1);
+        compute(q, b0, s0);
+        if (q + 1 >= nq) break;
+        if (q + 2 < nq) load_chunk(q + 2, b0, s0);
+        compute(q + 1, b1, s1);
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// CU-resident variant (exact FP8, router-ids mode): one 1024-thread
+// workgroup per CU, and every CU takes an equal contiguous range of items
+// (16 weight rows of one hit expert each).  Such a range spans at most two
+// experts at decode shapes.  The CU stages the activation rows its items read
+// in LDS once, quantised per group of 128 and widened to bf16 (e4m3fn is a
+// subset of bf16):
+//  * STAGE_TOKENS_Q16 / STAGE_TOKENS_H16 (top_k > 1, the gate_up GEMM): all
+//    token rows, copied from the pre-quantised rows the routing launch wrote,
+//    or quantised here from bf16;
+//  * STAGE_SLOTS_H16 (top_k == 1, the down GEMM): the rows of the slots of
+//    the CU's experts, quantised here from bf16.  Row sets larger than the
+//    LDS budget are processed in windows.
+// After the staging barrier the 16 waves are independent workers: wave w
+// takes items w, w + 16, ... of the CU's range.  Per K-step a lane loads 32
+// weight bytes (MFMA A operand: weight row l % 16; two dwordx4, the only
+// vector-memory traffic of the loop) and reads the matching 32 bf16 token
+// values from LDS (B operand: token row l % 16 of the expert).  Weights are
+// widened exactly to bf16 and each 128-wide block is four bf16 MFMAs with
+// exact fp32 accumulation, then scaled by s_token[block] * s_weight[block].
+// Lane l ends with (weight rows 4 (l/16) .. +3) x (token l % 16): its four
+// outputs share one token and one weight block.  Lanes past the expert's
+// token count read row 0 and store nothing (MFMA output columns are
+// independent).
+enum : int { STAGE_TOKENS_Q16 = 0, STAGE_TOKENS_H16 = 1, STAGE_SLOTS_H16 = 2 };
+constexpr int kCuThreads = 1024;
+constexpr int kCuWaves = kCuThreads / 64;
+constexpr size_t kCuLdsMax = 160 * 1024;
+
+template <int KS>
+__host__ __device__ constexpr int cu_pitch() { return KS * 256 + 16; }  // bytes per staged bf16 row
+
+// LDS layout: sAct[E] sCnt[E] sOff[E] sList[M'] | sSc[cap][KS] | rows[cap][pitch]
+__host__ __device__ inline size_t cu_lists_bytes(int E, int64_t M) {
+  return ((size_t)3 * E + (size_t)((M + 3) & ~3ll)) * 4;
+}
+template <int KS>
+__host__ __device__ inline size_t cu_rows_off(int E, int64_t M, int cap) {
+  return (cu_lists_bytes(E, M) + (size_t)cap * KS * 4 + 15) & ~(size_t)15;
+}
+
+template <int EPI, int KS, int STAGE>
+__global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, int cap) {
+  constexpr int PITCH = cu_pitch<KS>();
+  constexpr int KC = KS % 2 == 0 ? 2 : (KS % 3 == 0 ? 3 : 1);  // K-steps per chunk
+  constexpr int CH = KS / KC;
+  constexpr bool TOKENS = STAGE != STAGE_SLOTS_H16;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int E = p.num_experts;
+  int* sAct = (int*)smem;
+  int* sCnt = sAct + E;
+  int* sOff = sCnt + E;
+  int* sList = sOff + E;
+  float* sSc = (float*)(smem + cu_lists_bytes(E, p.M));
+  uint8_t* sRows = smem + cu_rows_off<KS>(E, p.M, cap);
+  __shared__ int sNact;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+
+  build_expert_lists<kCuThreads>(p, tid, w, lane, sAct, sCnt, sOff, sList, &sNact);
+  const int n_act = sNact;
+  const int IPE = EPI == EPI_ACT ? p.inter / 8 : p.N / 16;  // items per expert
+  const int total = n_act * IPE;
+  const int T = (total + gridDim.x - 1) / gridDim.x;
+  const int i0 = blockIdx.x * T;
+  const int i1 = i0 + T < total ? i0 + T : total;
+  if (i0 >= i1) return;
+  const int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
+  const uint16_t* A16 = (const uint16_t*)p.A;
+  uint16_t* C = (uint16_t*)p.C;
+
+  // ---- staging: `nrows` rows; row j reads A row arow_of(j).
+  auto stage_copy_q16 = [&](int nrows) {
+    // Pre-quantised, widened rows: a copy (16-byte pieces, 8 per thread in flight).
+    constexpr int PPR = KS * 16;  // pieces per row
+    const int pieces = nrows * PPR;
+    for (int base = 0; base < pieces; base += kCuThreads * 8) {
+      v4i v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int pc = base + j * kCuThreads + tid;
+        const int r = pc / PPR, c = pc - r * PPR;
+        v[j] = pc < pieces ? *(const v4i*)(A16 + (int64_t)r * p.lda + c * 8) : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int pc = base + j * kCuThreads + tid;
+        const int r = pc / PPR, c = pc - r * PPR;
+        if (pc < pieces) *(v4i*)(sRows + r * PITCH + c * 16) = v[j];
+      }
+    }
+    for (int i = tid; i < nrows * KS; i += kCuThreads) {
+      const int r = i / KS, ks = i - r * KS;
+      sSc[i] = p.a_scale[(int64_t)r * p.ld_as + ks];
+    }
+  };
+  auto stage_quant = [&](int nrows, auto arow_of) {
+    // bf16 rows quantised per group of 128 (16 lanes per group), widened.
+    constexpr int B = 2;
+    const int groups = nrows * KS;
+    for (int g0 = 0; g0 < groups; g0 += (kCuThreads / 16) * B) {
+      v4i raw[B];
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        const int gq = g0 + j * (kCuThreads / 16) + (tid >> 4), sub = tid & 15;
+        const bool live = gq < groups;
+        const int r = live ? gq / KS : 0, ks = live ? gq - (gq / KS) * KS : 0;
+        raw[j] = live ? *(const v4i*)(A16 + (int64_t)arow_of(r) * p.lda + ks * 128 + sub * 8)
+                      : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        const int gq = g0 + j * (kCuThreads / 16) + (tid >> 4), sub = tid & 15;
+        const bool live = gq < groups;
+        const int r = live ? gq / KS : 0, ks = live ? gq - (gq / KS) * KS : 0;
+        float sc;
+        const int2 codes = quant_group8<kBF16>(raw[j], sc);
+        if (live) {
+          *(v4i*)(sRows + r * PITCH + ks * 256 + sub * 16) = fp8x8_to_bf16x8_bits(codes.x, codes.y);
+          if (sub == 0) sSc[r * KS + ks] = sc;
+        }
+      }
+    }
+  };
+
+  // ---- items of experts [wa0, wa1] of this CU's range; for a single split
+  // expert only its rows [wr0, wr1).  LDS row of list entry i: i - lbase
+  // (slot rows) or the slot's token (token rows).
+  auto process = [&](int wa0, int wa1, int wr0, int wr1, int lbase) {
+    for (int it = i0 + w; it < i1; it += kCuWaves) {
+      const int a = it / IPE, g = it - a * IPE;
+      if (a < wa0 || a > wa1) continue;
+      const int e = sAct[a];
+      const int cnt = sCnt[e], off = sOff[e];
+      const int rb = a == wa0 ? wr0 : 0;
+      const int re = (a == wa0 && wr1 < cnt) ? wr1 : cnt;
+      const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride;
+      const float* Se = (const float*)p.b_scale + (int64_t)e * p.bs_estride;
+      // This lane's weight row; the weight-block rows of its outputs
+      // (rows 4 lg .. 4 lg + 3): gate block for lg < 2, up block above.
+      int br, blk_lo, blk_hi;
+      if constexpr (EPI == EPI_ACT) {
+        br = l16 < 8 ? g * 8 + l16 : p.inter + g * 8 + (l16 - 8);
+        blk_lo = (g * 8) / 128;
+        blk_hi = (p.inter + g * 8) / 128;
+      } else {
+        br = g * 16 + l16;
+        blk_lo = blk_hi = (g * 16) / 128;
+      }
+      const uint8_t* wsrc = Be + (int64_t)br * p.ldb + lg * 32;
+      const float* ws_lo = Se + (int64_t)__builtin_amdgcn_readfirstlane(blk_lo) * p.bs_ld;
+      const float* ws_hi = Se + (int64_t)__builtin_amdgcn_readfirstlane(blk_hi) * p.bs_ld;
+
+      for (int r0 = rb; r0 < re; r0 += 16) {
+        const int rows = re - r0 < 16 ? re - r0 : 16;
+        const bool tok_ok = l16 < rows;
+        const int li = off + r0 + (tok_ok ? l16 : 0);
+        const int slot = sList[li];
+        const int lrow = TOKENS ? slot / p.top_k : li - lbase;
+        const uint8_t* trow = sRows + lrow * PITCH + lg * 64;
+        const float* tsc = sSc + lrow * KS;
+
+        v8i wb0[KC], wb1[KC];
+        float f0[KC], f1[KC];
+        auto load = [&](int c, v8i (&wb)[KC], float (&f)[KC]) {
+#pragma unroll
+          for (int kk = 0; kk < KC; ++kk) {
+            const int ks = c * KC + kk;
+            wb[kk] = *(const v8i*)(wsrc + ks * 128);
+            const float lo = ws_lo[ks], hi = ws_hi[ks];
+            f[kk] = lg < 2 ? lo : hi;
+          }
+        };
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+        auto compute = [&](int c, const v8i (&wb)[KC], const float (&f)[KC]) {
+#pragma unroll
+          for (int kk = 0; kk < KC; ++kk) {
+            const int ks = c * KC + kk;
+            v4f t = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              t = mfma_bf16_16x16x32(fp8x8_to_bf16x8(wb[kk][2 * q], wb[kk][2 * q + 1]),
+                                     *(const v8s*)(trow + ks * 256 + q * 16), t);
+            acc += t * (tsc[ks] * f[kk]);
+          }
+        };
+        load(0, wb0, f0);
+#pragma unroll 1
+        for (int c = 0; c < CH; c += 2) {
+          if (c + 1 < CH) load(c + 1, wb1, f1);
+          compute(c, wb0, f0);
+          if (c + 1 >= CH) break;
+          if (c + 2 < CH) load(c + 2, wb0, f0);
+          compute(c + 1, wb1, f1);
+        }
+        // ---- epilogue: lane (l16, lg) holds weight rows 4 lg + r for token l16.
+        if constexpr (EPI == EPI_ACT) {
+          // Gate rows 0-7 sit in lanes lg 0-1, the matching up rows 32 lanes up.
+          float up[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(acc[r], 32, 64);
+          if (lg < 2 && tok_ok) {
+            uint32_t pk[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              uint32_t two = 0;
+#pragma unroll
+              for (int q = 0; q < 2; ++q) {
+                const int r = 2 * h + q;
+                const float gg = round_bf16(acc[r]);
+                const float u = round_bf16(up[r]);
+                const float av = round_bf16(p.activation == 0 ? act_f32<0>(gg) : act_f32<1>(gg));
+                two |= (uint32_t)f32_to_bf16_bits(av * u) << (16 * q);
+              }
+              pk[h] = two;
+            }
+            *(uint2*)(C + (int64_t)slot * p.ldc + g * 8 + 4 * lg) = make_uint2(pk[0], pk[1]);
+          }
+        } else {
+          if (tok_ok) {
+            const float rw = p.mul_routed ? load_weight_any(p.topk_w, p.topk_w_dtype, slot) : 1.f;
+            const uint32_t lo = (uint32_t)f32_to_bf16_bits(acc[0] * rw) |
+                                ((uint32_t)f32_to_bf16_bits(acc[1] * rw) << 16);
+            const uint32_t hi = (uint32_t)f32_to_bf16_bits(acc[2] * rw) |
+                                ((uint32_t)f32_to_bf16_bits(acc[3] * rw) << 16);
+            *(uint2*)(C + (int64_t)slot * p.ldc + g * 16 + 4 * lg) = make_uint2(lo, hi);
+          }
+        }
+      }
+    }
+  };
+
+  if constexpr (TOKENS) {
+    // All token rows (the host checked they fit): one staging, one barrier.
+    const int ntok = (int)((p.M + p.top_k - 1) / p.top_k);
+    if constexpr (STAGE == STAGE_TOKENS_Q16) stage_copy_q16(ntok);
+    else stage_quant(ntok, [&](int r) { return r; });
+    __syncthreads();
+    process(a_first, a_last, 0, 0x7fffffff, 0);
+  } else {
+    // Windows over the CU's experts: as many whole experts as fit in `cap`
+    // rows, or `cap` rows of one larger expert.  Usually a single window.
+    int a = a_first, r = 0;
+    while (a <= a_last) {
+      const int wa0 = a, wr0 = r;
+      int wa1 = a, wr1 = 0x7fffffff, nrows;
+      const int rem = sCnt[sAct[a]] - r;
+      if (rem > cap) {
+        nrows = cap;
+        wr1 = r + cap;
+        r += cap;
+      } else {
+        nrows = rem;
+        ++a;
+        r = 0;
+        while (a <= a_last && nrows + sCnt[sAct[a]] <= cap) {
+          nrows += sCnt[sAct[a]];
+          wa1 = a;
+          ++a;
+        }
+      }
+      const int lbase = sOff[sAct[wa0]] + wr0;  // list index of staged row 0
+      __syncthreads();                           // the previous window is done with LDS
+      stage_quant(nrows, [&](int j) { return sList[lbase + j] / p.top_k; });
+      __syncthreads();
+      process(wa0, wa1, wr0, wr1, lbase);
     }
   }
 }
@@ -287,13 +622,13 @@ static int num_cu() {
   return g_num_cu;
 }
 
-template <int EPI, int KS, bool EXACT>
+template <int EPI, int KS, bool EXACT, bool AQ>
 static int run_stream_fp8(const GemmArgs& a, hipStream_t stream) {
   constexpr int K = KS * 128;
   const size_t shmem = (size_t)kStreamRows * (K + 16) + (size_t)KS * kStreamRows * 4 +
                        kStreamRows * 4 + (size_t)a.num_experts * 3 * 4 +
                        (a.topk_ids ? (size_t)a.M * 4 : 0);
-  auto kern = stream_fp8_kernel<EPI, KS, EXACT>;
+  auto kern = stream_fp8_kernel<EPI, KS, EXACT, AQ>;
   static size_t attr_bytes = 0;  // largest LDS size opted in so far
   if (shmem > attr_bytes) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -303,9 +638,75 @@ static int run_stream_fp8(const GemmArgs& a, hipStream_t stream) {
     }
     attr_bytes = shmem;
   }
-  const int grid = kStreamWgPerCu * num_cu();
+  // Persistent: as many workgroups as can be resident (at most four per CU).
+  static int occ = 0;
+  if (occ <= 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)kern, 256, shmem) != hipSuccess ||
+        occ <= 0)
+      occ = 1;
+    if (occ > kStreamWgPerCu) occ = kStreamWgPerCu;
+  }
+  const int grid = occ * num_cu();
   kern<<<dim3(grid), dim3(256), shmem, stream>>>(a);
   return launch_status("stream_fp8");
+}
+
+template <int EPI, int KS, int STAGE>
+static int run_stream_fp8_cu(const GemmArgs& a, int cap, size_t shmem, hipStream_t stream) {
+  auto kern = stream_fp8_cu_kernel<EPI, KS, STAGE>;
+  static size_t attr_bytes = 0;
+  if (shmem > attr_bytes) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)shmem) != hipSuccess) {
+      set_last_error("stream_fp8_cu: cannot reserve %zu bytes of LDS", shmem);
+      return kLaunchError;
+    }
+    attr_bytes = shmem;
+  }
+  kern<<<dim3(num_cu()), dim3(kCuThreads), shmem, stream>>>(a, cap);
+  return launch_status("stream_fp8_cu");
+}
+
+// The CU-resident kernel for (exact, router-ids mode), or false if the shape
+// does not fit it.
+template <int KS>
+static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, int* status) {
+  const size_t lists = cu_lists_bytes(a.num_experts, a.M);
+  const size_t per_row = (size_t)cu_pitch<KS>() + KS * 4;
+  if (a.top_k > 1) {
+    // Token rows: all of them must fit.
+    const int ntok = (int)((a.M + a.top_k - 1) / a.top_k);
+    const size_t shmem = cu_rows_off<KS>(a.num_experts, a.M, ntok) + (size_t)ntok * cu_pitch<KS>();
+    if (shmem > kCuLdsMax - 1024) return false;
+    int stage;
+    if (a.a_scale && a.a_q16) stage = STAGE_TOKENS_Q16;
+    else if (!a.a_scale) stage = STAGE_TOKENS_H16;
+    else return false;
+    if (stage == STAGE_TOKENS_Q16)
+      *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_TOKENS_Q16>(a, ntok, shmem, stream)
+                               : run_stream_fp8_cu<EPI_STORE, KS, STAGE_TOKENS_Q16>(a, ntok, shmem, stream);
+    else
+      *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_TOKENS_H16>(a, ntok, shmem, stream)
+                               : run_stream_fp8_cu<EPI_STORE, KS, STAGE_TOKENS_H16>(a, ntok, shmem, stream);
+    return true;
+  }
+  if (a.a_scale) return false;  // slot rows are quantised while staged
+  // Slot rows: as many as the LDS budget allows (windows beyond that).
+  const size_t avail = kCuLdsMax - 1024 - lists - 16;
+  int cap = (int)(avail / per_row);
+  if (cap > 1024) cap = 1024;
+  if (cap < 16) return false;
+  const size_t shmem = cu_rows_off<KS>(a.num_experts, a.M, cap) + (size_t)cap * cu_pitch<KS>();
+  *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_SLOTS_H16>(a, cap, shmem, stream)
+                           : run_stream_fp8_cu<EPI_STORE, KS, STAGE_SLOTS_H16>(a, cap, shmem, stream);
+  return true;
+}
+
+bool stream_fp8_tokens_fit(int64_t tokens, int K, int E, int64_t slots) {
+  if (K % 128 != 0 || K / 128 > 16) return false;
+  const size_t lists = ((size_t)3 * E + (size_t)((slots + 3) & ~3ll)) * 4;
+  const size_t need = lists + (size_t)tokens * (K / 128) * 4 + 16 + (size_t)tokens * (K * 2 + 16);
+  return need <= kCuLdsMax - 1024;
 }
 
 bool stream_fp8_supported(int K, int N, int inter, int epi) {
@@ -324,11 +725,40 @@ int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream
   }
 #define MSTAR_SF8(KS)                                                                       \
   case KS:                                                                                  \
-    if (exact)                                                                              \
-      return epi == EPI_ACT ? run_stream_fp8<EPI_ACT, KS, true>(a, stream)                  \
-                            : run_stream_fp8<EPI_STORE, KS, true>(a, stream);               \
-    return epi == EPI_ACT ? run_stream_fp8<EPI_ACT, KS, false>(a, stream)                   \
-                          : run_stream_fp8<EPI_STORE, KS, false>(a, stream);
+    if (!exact)                                                                             \
+      return epi == EPI_ACT ? run_stream_fp8<EPI_ACT, KS, false, false>(a, stream)          \
+                            : run_stream_fp8<EPI_STORE, KS, false, false>(a, stream);       \
+    if (aq)                                                                                 \
+      return epi == EPI_ACT ? run_stream_fp8<EPI_ACT, KS, true, true>(a, stream)            \
+                            : run_stream_fp8<EPI_STORE, KS, true, true>(a, stream);         \
+    return epi == EPI_ACT ? run_stream_fp8<EPI_ACT, KS, true, false>(a, stream)             \
+                          : run_stream_fp8<EPI_STORE, KS, true, false>(a, stream);
+  // A with a_scale: e4m3fn rows already quantised per group of 128;
+  // otherwise bf16 rows, quantised while they are staged.
+  const bool aq = a.a_scale != nullptr;
+  if (aq && !exact) {
+    set_last_error("stream_fp8: pre-quantised activations need the exact path");
+    return kUnsupported;
+  }
+  if (exact && a.topk_ids && a.M <= kStreamMaxIdsSlots) {
+    int st = kOk;
+    bool done = false;
+    switch (a.K / 128) {
+      case 1: done = try_stream_fp8_cu<1>(a, epi, stream, &st); break;
+      case 2: done = try_stream_fp8_cu<2>(a, epi, stream, &st); break;
+      case 3: done = try_stream_fp8_cu<3>(a, epi, stream, &st); break;
+      case 4: done = try_stream_fp8_cu<4>(a, epi, stream, &st); break;
+      case 6: done = try_stream_fp8_cu<6>(a, epi, stream, &st); break;
+      case 8: done = try_stream_fp8_cu<8>(a, epi, stream, &st); break;
+      case 12: done = try_stream_fp8_cu<12>(a, epi, stream, &st); break;
+      case 16: done = try_stream_fp8_cu<16>(a, epi, stream, &st); break;
+    }
+    if (done) return st;
+  }
+  if (a.a_q16) {
+    set_last_error("stream_fp8: widened activations need the CU-resident kernel (shape too large)");
+    return kUnsupported;
+  }
   switch (a.K / 128) {
     MSTAR_SF8(1)
     MSTAR_SF8(2)

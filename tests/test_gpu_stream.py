@@ -1,0 +1,142 @@
+"""Decode entry points driven directly by the router ids (no alignment step):
+mstar_moe_topk_softmax_quant and mstar_moe_stream_gemm, composed the way the
+reference runner composes its stages (mstar/utils/fused_moe/runner.py:99-159)
+and checked against the CPU oracle."""
+from __future__ import annotations
+
+import functools
+
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+from tests._util import assert_moe_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+H, E, I, K_TOP = 2048, 128, 768, 8
+
+
+@functools.lru_cache(maxsize=1)
+def _weights():
+    from mstar_amd import quant
+    g = torch.Generator().manual_seed(11)
+    w1 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(DEV)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(DEV)
+    q1, s1 = quant.quantize_fp8_block(w1)
+    q2, s2 = quant.quantize_fp8_block(w2)
+    return q1, s1, q2, s2
+
+
+def _inputs(M, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    logits = torch.randn(M, E, generator=g)
+    return x, logits
+
+
+def _ref(x, tw, ti):
+    q1, s1, q2, s2 = (t.cpu() for t in _weights())
+    d1 = lambda e: O.dequant_fp8_block(q1[e], s1[e])
+    d2 = lambda e: O.dequant_fp8_block(q2[e], s2[e])
+    return O.fused_experts_rounding(x, None, None, tw, ti, w1_dq=d1, w2_dq=d2, act_quant=True)
+
+
+def _route_quant(x, logits):
+    from mstar_amd import _lib
+    lib = _lib.load()
+    M = x.shape[0]
+    tw = torch.empty(M, K_TOP, dtype=torch.float32, device=DEV)
+    ti = torch.empty(M, K_TOP, dtype=torch.int32, device=DEV)
+    hq = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    hs = torch.empty(M, H // 128, dtype=torch.float32, device=DEV)
+    xd, ld = x.to(DEV), logits.to(DEV)
+    _lib.check(lib.mstar_moe_topk_softmax_quant(
+        ld.data_ptr(), _lib.DT_F32, M, E, K_TOP, 1, tw.data_ptr(), ti.data_ptr(), None,
+        xd.data_ptr(), H, hq.data_ptr(), hs.data_ptr(), _lib.stream_of(xd)), "topk_softmax_quant")
+    return tw, ti, hq, hs
+
+
+def _stream_gemm(A, a_dt, a_scale, B, b_scale, C, tw, ti, slots, N, Kd, top_k, mul, act):
+    from mstar_amd import _lib
+    lib = _lib.load()
+    _lib.check(lib.mstar_moe_stream_gemm(
+        A.data_ptr(), a_dt, _lib.ptr(a_scale), B.data_ptr(), b_scale.data_ptr(), C.data_ptr(),
+        tw.data_ptr(), _lib.DT_F32, ti.data_ptr(), _lib.dtype_code(ti.dtype), slots, E, N, Kd,
+        top_k, mul, act, _lib.stream_of(A)), "moe_stream_gemm")
+
+
+def test_topk_softmax_quant_bit_exact():
+    """Routing equals mstar_moe_topk_softmax; the widened codes and scales
+    equal the per-token-group quantisation of the oracle bit for bit."""
+    from mstar_amd import ops
+    x, logits = _inputs(32, seed=1)
+    tw, ti, hq, hs = _route_quant(x, logits)
+    tw2, ti2 = ops.topk_softmax(logits.to(DEV), K_TOP, True)
+    assert torch.equal(ti.long(), ti2)
+    assert torch.equal(tw, tw2)
+    q_ref, s_ref = O.quant_fp8_per_token_group(x, 128)
+    assert torch.equal(hq.cpu().float(), q_ref.float())
+    assert torch.equal(hs.cpu(), s_ref)
+
+
+@pytest.mark.parametrize("M,a_mode,ids64", [(32, "q16", False), (32, "bf16", True), (1, "q16", False),
+                                            (24, "q16", True), (64, "bf16", True), (7, "bf16", False)])
+def test_stream_gemm_decode_layer(M, a_mode, ids64):
+    """topk+quant -> gate_up (fused SiLU-and-mul) -> down x routed weight ->
+    top-k sum, all through the C-ABI, against the oracle."""
+    from mstar_amd import _lib, ops
+    q1, s1, q2, s2 = _weights()
+    x, logits = _inputs(M, seed=100 + M)
+    tw, ti, hq, hs = _route_quant(x, logits)
+    ids = ti.long() if ids64 else ti
+    slots = M * K_TOP
+    c2 = torch.empty(slots, I, dtype=torch.bfloat16, device=DEV)
+    c3 = torch.empty(slots, H, dtype=torch.bfloat16, device=DEV)
+    if a_mode == "q16":
+        _stream_gemm(hq, _lib.DT_FP8_AS_BF16, hs, q1, s1, c2, tw, ids, slots, 2 * I, H, K_TOP, 0, 0)
+    else:
+        _stream_gemm(x.to(DEV), _lib.DT_BF16, None, q1, s1, c2, tw, ids, slots, 2 * I, H, K_TOP, 0, 0)
+    _stream_gemm(c2, _lib.DT_BF16, None, q2, s2, c3, tw, ids, slots, H, I, 1, 1, -1)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    ops.moe_sum_reduce(c3.view(M, K_TOP, H), out, 1.0)
+    ref = _ref(x, tw.cpu(), ti.cpu().long())
+    assert_moe_close(out, ref, what=f"stream gemm M={M} A={a_mode}")
+
+
+def test_stream_gemm_skewed_routing_uses_windows():
+    """Every token routed to the same 8 experts (128 slots each): the down
+    GEMM's per-CU row set exceeds its LDS budget and is processed in
+    windows; the gate_up GEMM (128 token rows) takes the LDS-staged kernel."""
+    from mstar_amd import _lib, ops
+    q1, s1, q2, s2 = _weights()
+    M = 128
+    x, _ = _inputs(M, seed=5)
+    g = torch.Generator().manual_seed(6)
+    ti = torch.stack([torch.randperm(8, generator=g) for _ in range(M)]).int()
+    tw = torch.softmax(torch.randn(M, K_TOP, generator=g), dim=-1)
+    slots = M * K_TOP
+    c2 = torch.empty(slots, I, dtype=torch.bfloat16, device=DEV)
+    c3 = torch.empty(slots, H, dtype=torch.bfloat16, device=DEV)
+    twd, tid = tw.to(DEV), ti.to(DEV)
+    _stream_gemm(x.to(DEV), _lib.DT_BF16, None, q1, s1, c2, twd, tid, slots, 2 * I, H, K_TOP, 0, 0)
+    _stream_gemm(c2, _lib.DT_BF16, None, q2, s2, c3, twd, tid, slots, H, I, 1, 1, -1)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    ops.moe_sum_reduce(c3.view(M, K_TOP, H), out, 1.0)
+    ref = _ref(x, tw, ti.long())
+    assert_moe_close(out, ref, what="stream gemm skewed")
+
+
+def test_stream_gemm_rejects_widened_rows_that_do_not_fit():
+    """FP8_AS_BF16 activations need every token row in LDS: 128 rows of
+    2048 do not fit, and the call says so instead of falling back."""
+    from mstar_amd import _lib
+    q1, s1, _, _ = _weights()
+    M = 128
+    hq = torch.zeros(M, H, dtype=torch.bfloat16, device=DEV)
+    hs = torch.ones(M, H // 128, dtype=torch.float32, device=DEV)
+    ti = torch.zeros(M * K_TOP, dtype=torch.int32, device=DEV)
+    tw = torch.ones(M * K_TOP, dtype=torch.float32, device=DEV)
+    c2 = torch.empty(M * K_TOP, I, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.MstarError, match="widened"):
+        _stream_gemm(hq, _lib.DT_FP8_AS_BF16, hs, q1, s1, c2, tw, ti, M * K_TOP, 2 * I, H, K_TOP, 0, 0)
