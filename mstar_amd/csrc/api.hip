@@ -104,8 +104,7 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->off_c2 = take((size_t)pl->slots * I * 2);
   pl->off_c3 = reduce ? take((size_t)pl->slots * H * 2) : 0;
   const bool fp8_tiled = quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream;
-  pl->route_quant = with_route && pl->ids_mode && H % 512 == 0 &&
-                    stream_fp8_tokens_fit(M, (int)H, E, pl->slots);
+  pl->route_quant = with_route && pl->ids_mode && H % 512 == 0;
   pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;
   pl->off_hs = fp8_tiled || pl->route_quant ? take((size_t)M * (H / 128) * 4) : 0;
   pl->off_cq = fp8_tiled ? take((size_t)pl->slots * I) : 0;

@@ -115,6 +115,25 @@ __device__ __forceinline__ v4i fp8x8_to_bf16x8_bits(int x0, int x1) {
   return v4i{c0, c1, c2, c3};
 }
 
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt low
+// bits [3:0], high bits [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier without a memory fence (outstanding global loads and LDS
+// DMA stay in flight).  The memory clobber keeps the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Workgroup barrier that leaves outstanding global loads in flight: LDS
+// traffic is completed (lgkmcnt) but vmcnt is not drained, unlike the
+// workgroup fence of __syncthreads().  The memory clobber keeps the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Raw buffer resource over [base, base + bytes): buffer loads at offsets
 // >= bytes return zeros without a memory request, which is how lanes with
 // nothing to load are masked without a branch.

@@ -63,19 +63,6 @@ __device__ __forceinline__ v8i lds_frag_swz(const uint8_t* row_base, int row, in
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt low
-// bits [3:0], high bits [15:14], expcnt [6:4], lgkmcnt [11:8]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// Workgroup barrier without a memory fence.  The memory clobber keeps the
-// compiler from moving LDS accesses across it; the LDS-DMA data a wave
-// produced is complete once its own vmcnt wait has passed.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
 template <int EPI, bool GROUPED, bool BLOCKSCALE>
 __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   constexpr int BM = kBigBM, BN = kBigBN, WN = kBigWN, WTM = BM / kBigWM, WTN = BN / kBigWN;

@@ -115,9 +115,6 @@ constexpr int kBigBlockM = 256;
 int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream);
 constexpr int64_t kStreamMaxIdsSlots = 1024;  // slots a launch in ids mode can take
 bool stream_fp8_supported(int K, int N, int inter, int epi);
-// Whether `tokens` activation rows of K values, widened to bf16, fit the LDS
-// of the CU-resident streaming kernel (the condition for feeding it
-// pre-quantised widened rows).
-bool stream_fp8_tokens_fit(int64_t tokens, int K, int E, int64_t slots);
+
 
 }  // namespace mstar

@@ -339,111 +339,229 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// CU-resident variant (exact FP8, router-ids mode): one 1024-thread
+// CU-resident variant (exact FP8, router-ids mode): one 512-thread
 // workgroup per CU, and every CU takes an equal contiguous range of items
 // (16 weight rows of one hit expert each).  Such a range spans at most two
-// experts at decode shapes.  The CU stages the activation rows its items read
-// in LDS once, quantised per group of 128 and widened to bf16 (e4m3fn is a
-// subset of bf16):
-//  * STAGE_TOKENS_Q16 / STAGE_TOKENS_H16 (top_k > 1, the gate_up GEMM): all
-//    token rows, copied from the pre-quantised rows the routing launch wrote,
-//    or quantised here from bf16;
-//  * STAGE_SLOTS_H16 (top_k == 1, the down GEMM): the rows of the slots of
-//    the CU's experts, quantised here from bf16.  Row sets larger than the
-//    LDS budget are processed in windows.
-// After the staging barrier the 16 waves are independent workers: wave w
-// takes items w, w + 16, ... of the CU's range.  Per K-step a lane loads 32
-// weight bytes (MFMA A operand: weight row l % 16; two dwordx4, the only
-// vector-memory traffic of the loop) and reads the matching 32 bf16 token
-// values from LDS (B operand: token row l % 16 of the expert).  Weights are
-// widened exactly to bf16 and each 128-wide block is four bf16 MFMAs with
-// exact fp32 accumulation, then scaled by s_token[block] * s_weight[block].
-// Lane l ends with (weight rows 4 (l/16) .. +3) x (token l % 16): its four
-// outputs share one token and one weight block.  Lanes past the expert's
-// token count read row 0 and store nothing (MFMA output columns are
-// independent).
-enum : int { STAGE_TOKENS_Q16 = 0, STAGE_TOKENS_H16 = 1, STAGE_SLOTS_H16 = 2 };
-constexpr int kCuThreads = 1024;
+// experts at decode shapes.
+//  * Activation rows: the CU stages the rows of its experts' slots (A row =
+//    slot / top_k) in LDS once, quantised per group of 128 and widened to
+//    bf16 (e4m3fn is a subset of bf16): copied from pre-quantised widened
+//    rows (STAGE_Q16, as the routing launch writes them) or quantised here
+//    from bf16 (STAGE_H16).  Row sets beyond the LDS budget are processed in
+//    windows.
+//  * Weights: each wave streams its items through a private three-slot LDS
+//    ring with LDS-DMA loads (global_load_lds_dwordx4).  One instruction
+//    fetches 8 weight rows x 128 bytes -- whole 128-byte lines, the access
+//    shape that streams fastest -- with the streaming cache policy; the 16
+//    bytes of lane l land at slot + 16 l (row l / 8, physical chunk l % 8,
+//    holding logical chunk (l % 8) ^ row, so the fragment reads below are
+//    bank-conflict free).  Two chunks are in flight while one computes; the
+//    waits are per wave (vmcnt), so the main loop has no workgroup barrier.
+//  * Math: lane l reads weight row l % 16, K bytes 32 (l / 16) .. +31 of a
+//    K-step from the ring (MFMA A operand) and the matching 32 bf16 token
+//    values from the staged rows (B operand: token row l % 16 of the
+//    expert).  Weights are widened exactly to bf16; each 128-wide block is
+//    four bf16 MFMAs with exact fp32 accumulation, scaled by
+//    s_token[block] * s_weight[block].  Lane l ends with (weight rows
+//    4 (l/16) .. +3) x (token l % 16).  Lanes past the expert's token count
+//    read row 0 and store nothing (MFMA output columns are independent).
+enum : int { STAGE_Q16 = 0, STAGE_H16 = 1 };
+constexpr int kCuThreads = 512;
 constexpr int kCuWaves = kCuThreads / 64;
+constexpr int kCuStageWaves = 2;  // waves that stage rows; the others prefetch weights meanwhile
+constexpr int kCuRing = 3;        // ring slots per wave
 constexpr size_t kCuLdsMax = 160 * 1024;
+constexpr int kDmaAux = 2;        // cache policy of the weight stream (streaming)
 
 template <int KS>
-__host__ __device__ constexpr int cu_pitch() { return KS * 256 + 16; }  // bytes per staged bf16 row
-
-// LDS layout: sAct[E] sCnt[E] sOff[E] sList[M'] | sSc[cap][KS] | rows[cap][pitch]
+__host__ __device__ constexpr int cu_kc() { return KS % 2 == 0 ? 2 : KS; }  // K-steps per chunk
+template <int KS>
+__host__ __device__ constexpr int cu_pitch() { return KS * 256 + 16; }     // bytes per staged bf16 row
+template <int KS>
+__host__ __device__ constexpr size_t cu_ring_bytes() {
+  return (size_t)kCuWaves * kCuRing * cu_kc<KS>() * 2048;
+}
+// LDS layout: rings | sAct[E] sCnt[E] sOff[E] sList[M'] | sSc[cap][KS] sRw[cap] |
+// rows[cap][pitch]
 __host__ __device__ inline size_t cu_lists_bytes(int E, int64_t M) {
   return ((size_t)3 * E + (size_t)((M + 3) & ~3ll)) * 4;
 }
 template <int KS>
+__host__ __device__ inline size_t cu_sc_off(int E, int64_t M) {
+  return cu_ring_bytes<KS>() + cu_lists_bytes(E, M);
+}
+template <int KS>
 __host__ __device__ inline size_t cu_rows_off(int E, int64_t M, int cap) {
-  return (cu_lists_bytes(E, M) + (size_t)cap * KS * 4 + 15) & ~(size_t)15;
+  return (cu_sc_off<KS>(E, M) + (size_t)cap * (KS + 1) * 4 + 15) & ~(size_t)15;
 }
 
 template <int EPI, int KS, int STAGE>
 __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, int cap) {
   constexpr int PITCH = cu_pitch<KS>();
-  constexpr int KC = KS % 2 == 0 ? 2 : (KS % 3 == 0 ? 3 : 1);  // K-steps per chunk
-  constexpr int CH = KS / KC;
-  constexpr bool TOKENS = STAGE != STAGE_SLOTS_H16;
+  constexpr int KC = cu_kc<KS>();
+  constexpr int CH = KS / KC;         // chunks per item
+  constexpr int SLOT = KC * 2048;     // ring slot bytes
+  constexpr int DPC = 2 * KC;         // DMA instructions per chunk
+  constexpr int SPT = (int)(kStreamMaxIdsSlots / kCuThreads);  // router ids per thread
+  typedef __attribute__((address_space(3))) void* lds_void_ptr;
   extern __shared__ __align__(16) uint8_t smem[];
   const int E = p.num_experts;
-  int* sAct = (int*)smem;
+  int* sAct = (int*)(smem + cu_ring_bytes<KS>());
   int* sCnt = sAct + E;
   int* sOff = sCnt + E;
   int* sList = sOff + E;
-  float* sSc = (float*)(smem + cu_lists_bytes(E, p.M));
+  float* sSc = (float*)(smem + cu_sc_off<KS>(E, p.M));
+  float* sRw = sSc + cap * KS;  // routed weight of each staged row
   uint8_t* sRows = smem + cu_rows_off<KS>(E, p.M, cap);
-  __shared__ int sNact;
+  __shared__ uint32_t sMask[32];  // active experts (E <= 1024)
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
-
-  build_expert_lists<kCuThreads>(p, tid, w, lane, sAct, sCnt, sOff, sList, &sNact);
-  const int n_act = sNact;
   const int IPE = EPI == EPI_ACT ? p.inter / 8 : p.N / 16;  // items per expert
+  const uint16_t* A16 = (const uint16_t*)p.A;
+  uint16_t* C = (uint16_t*)p.C;
+  uint8_t* ring = smem + w * (kCuRing * SLOT);
+
+  // ---- prologue 1: per-expert counts and the active-expert mask.
+  for (int e = tid; e < E; e += kCuThreads) sCnt[e] = 0;
+  if (tid < 32) sMask[tid] = 0;
+  lds_sync();
+  int my_e[SPT], my_pos[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    const int i = tid + j * kCuThreads;
+    int e = -1;
+    if (i < p.M) {
+      const int64_t v = p.ids_dtype == kI64 ? ((const int64_t*)p.topk_ids)[i]
+                                            : (int64_t)((const int32_t*)p.topk_ids)[i];
+      e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are skipped (.cu:44-46)
+    }
+    my_e[j] = e;
+    my_pos[j] = 0;
+    if (e >= 0) {
+      my_pos[j] = atomicAdd(&sCnt[e], 1);
+      atomicOr(&sMask[e >> 5], 1u << (e & 31));
+    }
+  }
+  lds_sync();
+  // Active experts: prefix popcounts of the mask words (lane i: word i).
+  const uint32_t mword = lane < 32 ? sMask[lane] : 0u;
+  const int wincl = wave_incl_scan(__builtin_popcount(mword));
+  const int n_act = __shfl(wincl, 63, 64);
   const int total = n_act * IPE;
   const int T = (total + gridDim.x - 1) / gridDim.x;
   const int i0 = blockIdx.x * T;
   const int i1 = i0 + T < total ? i0 + T : total;
   if (i0 >= i1) return;
-  const int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
-  const uint16_t* A16 = (const uint16_t*)p.A;
-  uint16_t* C = (uint16_t*)p.C;
+  auto active_expert = [&](int a) -> int {  // the a-th active expert (wave-uniform a)
+    const uint64_t past = __ballot(wincl > a);
+    const int word = __builtin_ctzll(past);
+    uint32_t m = (uint32_t)__shfl((int)mword, word, 64);
+    int skip = a - (__shfl(wincl, word, 64) - __builtin_popcount(m));
+    for (; skip > 0; --skip) m &= m - 1u;
+    return word * 32 + __builtin_ctz(m);
+  };
 
-  // ---- staging: `nrows` rows; row j reads A row arow_of(j).
-  auto stage_copy_q16 = [&](int nrows) {
-    // Pre-quantised, widened rows: a copy (16-byte pieces, 8 per thread in flight).
-    constexpr int PPR = KS * 16;  // pieces per row
-    const int pieces = nrows * PPR;
-    for (int base = 0; base < pieces; base += kCuThreads * 8) {
-      v4i v[8];
+  // ---- weight DMA of (item, chunk) into ring slot `slot`.  DMA lane geometry:
+  // rows r8 and 8 + r8 of the item, physical chunk pc = logical pc ^ r8.
+  const int r8 = lane >> 3;
+  const uint32_t lc16 = (uint32_t)(((lane & 7) ^ r8) * 16);
+  auto dma_rows = [&](int e, int g, const uint8_t*& s0, const uint8_t*& s1) {
+    const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride;
+    int row0, row1;
+    if constexpr (EPI == EPI_ACT) {
+      row0 = g * 8 + r8;
+      row1 = p.inter + g * 8 + r8;
+    } else {
+      row0 = g * 16 + r8;
+      row1 = g * 16 + 8 + r8;
+    }
+    s0 = Be + (int64_t)row0 * p.ldb + lc16;
+    s1 = Be + (int64_t)row1 * p.ldb + lc16;
+  };
+  auto dma = [&](const uint8_t* s0, const uint8_t* s1, int c, int slot) {
+    uint8_t* dst = ring + slot * SLOT;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int pc = base + j * kCuThreads + tid;
+    for (int kk = 0; kk < KC; ++kk) {
+      __builtin_amdgcn_global_load_lds((const void*)(s0 + (c * KC + kk) * 128),
+                                       (lds_void_ptr)(dst + kk * 2048), 16, 0, kDmaAux);
+      __builtin_amdgcn_global_load_lds((const void*)(s1 + (c * KC + kk) * 128),
+                                       (lds_void_ptr)(dst + kk * 2048 + 1024), 16, 0, kDmaAux);
+    }
+  };
+
+  // ---- prefetch: waves that do not stage start their first item's weights
+  // now; lds_sync leaves the DMA in flight through the rest of the prologue.
+  const int it_first = i0 + w;
+  const bool prefetched = w >= kCuStageWaves && it_first < i1;
+  if (prefetched) {
+    const int a = it_first / IPE;
+    const uint8_t *s0, *s1;
+    dma_rows(active_expert(a), it_first - a * IPE, s0, s1);
+#pragma unroll
+    for (int c = 0; c < kCuRing - 1; ++c)
+      if (c < CH) dma(s0, s1, c, c);
+  }
+
+  // ---- prologue 2: offsets, active list, slot lists.
+  if (w == 0) {
+    int run = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int c = e < E ? sCnt[e] : 0;
+      const int incl = wave_incl_scan(c);
+      if (e < E) sOff[e] = run + incl - c;
+      run += __shfl(incl, 63, 64);
+    }
+    int n = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const bool act = e < E && sCnt[e] > 0;
+      const uint64_t b = __ballot(act);
+      if (act) sAct[n + __builtin_popcountll(b & ((1ull << lane) - 1ull))] = e;
+      n += __builtin_popcountll(b);
+    }
+  }
+  lds_sync();
+#pragma unroll
+  for (int j = 0; j < SPT; ++j)
+    if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * kCuThreads;
+  lds_sync();
+  const int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
+
+  // ---- staging (waves < kCuStageWaves): `nrows` rows; row j reads A row arow_of(j).
+  constexpr int ST = kCuStageWaves * 64;
+  auto stage_copy_q16 = [&](int nrows, auto arow_of) {
+    constexpr int PPR = KS * 16;  // 16-byte pieces per row
+    const int pieces = nrows * PPR;
+    for (int base = 0; base < pieces; base += ST * 4) {
+      v4i v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pc = base + j * ST + tid;
         const int r = pc / PPR, c = pc - r * PPR;
-        v[j] = pc < pieces ? *(const v4i*)(A16 + (int64_t)r * p.lda + c * 8) : v4i{0, 0, 0, 0};
+        v[j] = pc < pieces ? *(const v4i*)(A16 + (int64_t)arow_of(r) * p.lda + c * 8) : v4i{0, 0, 0, 0};
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int pc = base + j * kCuThreads + tid;
+      for (int j = 0; j < 4; ++j) {
+        const int pc = base + j * ST + tid;
         const int r = pc / PPR, c = pc - r * PPR;
         if (pc < pieces) *(v4i*)(sRows + r * PITCH + c * 16) = v[j];
       }
     }
-    for (int i = tid; i < nrows * KS; i += kCuThreads) {
+    for (int i = tid; i < nrows * KS; i += ST) {
       const int r = i / KS, ks = i - r * KS;
-      sSc[i] = p.a_scale[(int64_t)r * p.ld_as + ks];
+      sSc[i] = p.a_scale[(int64_t)arow_of(r) * p.ld_as + ks];
     }
   };
   auto stage_quant = [&](int nrows, auto arow_of) {
-    // bf16 rows quantised per group of 128 (16 lanes per group), widened.
     constexpr int B = 2;
     const int groups = nrows * KS;
-    for (int g0 = 0; g0 < groups; g0 += (kCuThreads / 16) * B) {
+    for (int g0 = 0; g0 < groups; g0 += (ST / 16) * B) {
       v4i raw[B];
 #pragma unroll
       for (int j = 0; j < B; ++j) {
-        const int gq = g0 + j * (kCuThreads / 16) + (tid >> 4), sub = tid & 15;
+        const int gq = g0 + j * (ST / 16) + (tid >> 4), sub = tid & 15;
         const bool live = gq < groups;
         const int r = live ? gq / KS : 0, ks = live ? gq - (gq / KS) * KS : 0;
         raw[j] = live ? *(const v4i*)(A16 + (int64_t)arow_of(r) * p.lda + ks * 128 + sub * 8)
@@ -451,7 +569,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
       }
 #pragma unroll
       for (int j = 0; j < B; ++j) {
-        const int gq = g0 + j * (kCuThreads / 16) + (tid >> 4), sub = tid & 15;
+        const int gq = g0 + j * (ST / 16) + (tid >> 4), sub = tid & 15;
         const bool live = gq < groups;
         const int r = live ? gq / KS : 0, ks = live ? gq - (gq / KS) * KS : 0;
         float sc;
@@ -464,149 +582,236 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
     }
   };
 
-  // ---- items of experts [wa0, wa1] of this CU's range; for a single split
-  // expert only its rows [wr0, wr1).  LDS row of list entry i: i - lbase
-  // (slot rows) or the slot's token (token rows).
-  auto process = [&](int wa0, int wa1, int wr0, int wr1, int lbase) {
-    for (int it = i0 + w; it < i1; it += kCuWaves) {
-      const int a = it / IPE, g = it - a * IPE;
-      if (a < wa0 || a > wa1) continue;
-      const int e = sAct[a];
-      const int cnt = sCnt[e], off = sOff[e];
-      const int rb = a == wa0 ? wr0 : 0;
-      const int re = (a == wa0 && wr1 < cnt) ? wr1 : cnt;
-      const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride;
-      const float* Se = (const float*)p.b_scale + (int64_t)e * p.bs_estride;
-      // This lane's weight row; the weight-block rows of its outputs
-      // (rows 4 lg .. 4 lg + 3): gate block for lg < 2, up block above.
-      int br, blk_lo, blk_hi;
+  // ---- the wave's units in a window: (item, pass of up to 16 rows).  A
+  // cursor walks them; the issue cursor runs kCuRing - 1 chunks ahead of
+  // the compute cursor.
+  struct Cur {
+    int it, r0, c;  // item, first row of the pass, chunk
+  };
+  int wa0 = 0, wa1 = -1, wr0 = 0, wr1 = 0;
+  auto item_rows = [&](int it, int& rb, int& re) -> bool {  // row range of `it` in the window
+    const int a = it / IPE;
+    if (a < wa0 || a > wa1) return false;
+    const int cnt = __builtin_amdgcn_readfirstlane(sCnt[sAct[a]]);
+    rb = a == wa0 ? wr0 : 0;
+    re = (a == wa0 && wr1 < cnt) ? wr1 : cnt;
+    return rb < re;
+  };
+  auto first_unit = [&](int it, Cur& cu) -> bool {  // first unit at or after item `it`
+    for (; it < i1; it += kCuWaves) {
+      int rb, re;
+      if (item_rows(it, rb, re)) {
+        cu = Cur{it, rb, 0};
+        return true;
+      }
+    }
+    return false;
+  };
+  auto advance = [&](Cur& cu) -> bool {  // next chunk
+    if (++cu.c < CH) return true;
+    int rb, re;
+    item_rows(cu.it, rb, re);
+    if (cu.r0 + 16 < re) {
+      cu.r0 += 16;
+      cu.c = 0;
+      return true;
+    }
+    return first_unit(cu.it + kCuWaves, cu);
+  };
+
+  bool use_prefetch = prefetched;
+  auto run_window = [&](int lbase) {
+    Cur ic, cc;  // issue / compute cursors
+    bool ihas = first_unit(i0 + w, ic);
+    if (!ihas) {
+      if (use_prefetch) wait_vmcnt<0>();  // the prefetch targeted a later window: retire it
+      use_prefetch = false;
+      return;
+    }
+    cc = ic;
+    // Issue the first kCuRing - 1 chunks (or adopt the prefetch).
+    int ahead = 0;      // chunks issued beyond the compute cursor
+    int islot = 0;      // ring slot of the next issue
+    const uint8_t *is0, *is1;
+    int icur_it = -1, icur_r0 = -1;
+    auto issue_next = [&]() {
+      if (ic.it != icur_it || ic.r0 != icur_r0) {
+        const int a = ic.it / IPE;
+        dma_rows(sAct[a], ic.it - a * IPE, is0, is1);
+        icur_it = ic.it;
+        icur_r0 = ic.r0;
+      }
+      dma(is0, is1, ic.c, islot);
+      islot = islot + 1 == kCuRing ? 0 : islot + 1;
+      ++ahead;
+      ihas = advance(ic);
+    };
+    const bool adopt = use_prefetch && ic.it == it_first && ic.c == 0;
+    if (use_prefetch && !adopt) wait_vmcnt<0>();  // retire a prefetch this window does not use
+    use_prefetch = false;
+    for (int n = 0; n < kCuRing - 1 && ihas; ++n) {
+      if (adopt) {  // already in flight
+        if (ic.it != icur_it || ic.r0 != icur_r0) {
+          const int a = ic.it / IPE;
+          dma_rows(sAct[a], ic.it - a * IPE, is0, is1);
+          icur_it = ic.it;
+          icur_r0 = ic.r0;
+        }
+        if (ic.it != it_first || ic.r0 != cc.r0) break;  // the prefetch covered only the first unit
+        islot = islot + 1 == kCuRing ? 0 : islot + 1;
+        ++ahead;
+        ihas = advance(ic);
+      } else {
+        issue_next();
+      }
+    }
+    int cslot = 0;
+    while (true) {
+      // ---- unit set-up (compute side)
+      const int a = cc.it / IPE, g = cc.it - a * IPE;
+      const int e = __builtin_amdgcn_readfirstlane(sAct[a]);
+      const int off = __builtin_amdgcn_readfirstlane(sOff[e]);
+      int rb, re;
+      item_rows(cc.it, rb, re);
+      const int rows = re - cc.r0 < 16 ? re - cc.r0 : 16;
+      const bool tok_ok = l16 < rows;
+      const int li = off + cc.r0 + (tok_ok ? l16 : 0);
+      const int slot_id = sList[li];
+      const int lrow = li - lbase;
+      const uint8_t* trow = sRows + lrow * PITCH + lg * 64;
+      const float* tsc = sSc + lrow * KS;
+      // Element offsets of the weight-block scale rows of this unit's outputs
+      // (gate block for lanes lg < 2, up block above).
+      int blk_lo, blk_hi;
       if constexpr (EPI == EPI_ACT) {
-        br = l16 < 8 ? g * 8 + l16 : p.inter + g * 8 + (l16 - 8);
         blk_lo = (g * 8) / 128;
         blk_hi = (p.inter + g * 8) / 128;
       } else {
-        br = g * 16 + l16;
         blk_lo = blk_hi = (g * 16) / 128;
       }
-      const uint8_t* wsrc = Be + (int64_t)br * p.ldb + lg * 32;
-      const float* ws_lo = Se + (int64_t)__builtin_amdgcn_readfirstlane(blk_lo) * p.bs_ld;
-      const float* ws_hi = Se + (int64_t)__builtin_amdgcn_readfirstlane(blk_hi) * p.bs_ld;
-
-      for (int r0 = rb; r0 < re; r0 += 16) {
-        const int rows = re - r0 < 16 ? re - r0 : 16;
-        const bool tok_ok = l16 < rows;
-        const int li = off + r0 + (tok_ok ? l16 : 0);
-        const int slot = sList[li];
-        const int lrow = TOKENS ? slot / p.top_k : li - lbase;
-        const uint8_t* trow = sRows + lrow * PITCH + lg * 64;
-        const float* tsc = sSc + lrow * KS;
-
-        v8i wb0[KC], wb1[KC];
-        float f0[KC], f1[KC];
-        auto load = [&](int c, v8i (&wb)[KC], float (&f)[KC]) {
+      const int so_lo = (int)(e * p.bs_estride) + blk_lo * (int)p.bs_ld;
+      const int so_hi = (int)(e * p.bs_estride) + blk_hi * (int)p.bs_ld;
+      // Read-only for the whole launch: reading it through the constant
+      // address space lets the compiler use scalar loads.
+      typedef const __attribute__((address_space(4))) float* const_fptr;
+      const const_fptr bsc = (const_fptr)p.b_scale;
+      v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+      const int unit_it = cc.it, unit_r0 = cc.r0;
+      // ---- chunks of the unit
+      while (true) {
+        while (ihas && ahead < kCuRing) issue_next();
+        // Wait for this chunk's DMA, leaving the later ones in flight (two
+        // fewer, for the epilogue store / routed-weight load that may sit
+        // between them: over-waiting is safe).
+        if (ahead >= 3) wait_vmcnt<(2 * DPC - 2 > 0 ? 2 * DPC - 2 : 0)>();
+        else if (ahead == 2) wait_vmcnt<(DPC - 2 > 0 ? DPC - 2 : 0)>();
+        else wait_vmcnt<0>();
+        const uint8_t* wslot = ring + cslot * SLOT;
+        // Wave-uniform, so the weight-scale reads below are scalar loads (a
+        // vector load here would make the compiler drain the DMA queue).
+        const int c = __builtin_amdgcn_readfirstlane(cc.c);
 #pragma unroll
-          for (int kk = 0; kk < KC; ++kk) {
-            const int ks = c * KC + kk;
-            wb[kk] = *(const v8i*)(wsrc + ks * 128);
-            const float lo = ws_lo[ks], hi = ws_hi[ks];
-            f[kk] = lg < 2 ? lo : hi;
-          }
-        };
-        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-        auto compute = [&](int c, const v8i (&wb)[KC], const float (&f)[KC]) {
-#pragma unroll
-          for (int kk = 0; kk < KC; ++kk) {
-            const int ks = c * KC + kk;
-            v4f t = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              t = mfma_bf16_16x16x32(fp8x8_to_bf16x8(wb[kk][2 * q], wb[kk][2 * q + 1]),
-                                     *(const v8s*)(trow + ks * 256 + q * 16), t);
-            acc += t * (tsc[ks] * f[kk]);
-          }
-        };
-        load(0, wb0, f0);
-#pragma unroll 1
-        for (int c = 0; c < CH; c += 2) {
-          if (c + 1 < CH) load(c + 1, wb1, f1);
-          compute(c, wb0, f0);
-          if (c + 1 >= CH) break;
-          if (c + 2 < CH) load(c + 2, wb0, f0);
-          compute(c + 1, wb1, f1);
+        for (int kk = 0; kk < KC; ++kk) {
+          const int ks = c * KC + kk;
+          const uint8_t* wrow = wslot + kk * 2048 + l16 * 128;
+          const int sw = l16 & 7;
+          const v4i wlo = *(const v4i*)(wrow + (((2 * lg) ^ sw) << 4));
+          const v4i whi = *(const v4i*)(wrow + (((2 * lg + 1) ^ sw) << 4));
+          // Scalar loads: the indices are wave-uniform by construction.
+          const float slo = bsc[__builtin_amdgcn_readfirstlane(so_lo + ks)];
+          const float shi = bsc[__builtin_amdgcn_readfirstlane(so_hi + ks)];
+          const float f = tsc[ks] * (lg < 2 ? slo : shi);
+          v4f t = v4f{0.f, 0.f, 0.f, 0.f};
+          t = mfma_bf16_16x16x32(fp8x8_to_bf16x8(wlo[0], wlo[1]), *(const v8s*)(trow + ks * 256), t);
+          t = mfma_bf16_16x16x32(fp8x8_to_bf16x8(wlo[2], wlo[3]), *(const v8s*)(trow + ks * 256 + 16), t);
+          t = mfma_bf16_16x16x32(fp8x8_to_bf16x8(whi[0], whi[1]), *(const v8s*)(trow + ks * 256 + 32), t);
+          t = mfma_bf16_16x16x32(fp8x8_to_bf16x8(whi[2], whi[3]), *(const v8s*)(trow + ks * 256 + 48), t);
+          acc += t * f;
         }
-        // ---- epilogue: lane (l16, lg) holds weight rows 4 lg + r for token l16.
-        if constexpr (EPI == EPI_ACT) {
-          // Gate rows 0-7 sit in lanes lg 0-1, the matching up rows 32 lanes up.
-          float up[4];
+        cslot = cslot + 1 == kCuRing ? 0 : cslot + 1;
+        --ahead;
+        const bool more = advance(cc);
+        if (!more || cc.it != unit_it || cc.r0 != unit_r0) {
+          // ---- epilogue of the unit: lane (l16, lg) holds weight rows 4 lg + r for token l16.
+          if constexpr (EPI == EPI_ACT) {
+            // Gate rows 0-7 sit in lanes lg 0-1, the matching up rows 32 lanes up.
+            float up[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(acc[r], 32, 64);
-          if (lg < 2 && tok_ok) {
-            uint32_t pk[2];
+            for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(acc[r], 32, 64);
+            if (lg < 2 && tok_ok) {
+              uint32_t pk[2];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              uint32_t two = 0;
+              for (int h = 0; h < 2; ++h) {
+                uint32_t two = 0;
 #pragma unroll
-              for (int q = 0; q < 2; ++q) {
-                const int r = 2 * h + q;
-                const float gg = round_bf16(acc[r]);
-                const float u = round_bf16(up[r]);
-                const float av = round_bf16(p.activation == 0 ? act_f32<0>(gg) : act_f32<1>(gg));
-                two |= (uint32_t)f32_to_bf16_bits(av * u) << (16 * q);
+                for (int q = 0; q < 2; ++q) {
+                  const int r = 2 * h + q;
+                  const float gg = round_bf16(acc[r]);
+                  const float u = round_bf16(up[r]);
+                  const float av = round_bf16(p.activation == 0 ? act_f32<0>(gg) : act_f32<1>(gg));
+                  two |= (uint32_t)f32_to_bf16_bits(av * u) << (16 * q);
+                }
+                pk[h] = two;
               }
-              pk[h] = two;
+              *(uint2*)(C + (int64_t)slot_id * p.ldc + g * 8 + 4 * lg) = make_uint2(pk[0], pk[1]);
             }
-            *(uint2*)(C + (int64_t)slot * p.ldc + g * 8 + 4 * lg) = make_uint2(pk[0], pk[1]);
+          } else {
+            if (tok_ok) {
+              const float rw = p.mul_routed ? sRw[lrow] : 1.f;
+              const uint32_t lo = (uint32_t)f32_to_bf16_bits(acc[0] * rw) |
+                                  ((uint32_t)f32_to_bf16_bits(acc[1] * rw) << 16);
+              const uint32_t hi = (uint32_t)f32_to_bf16_bits(acc[2] * rw) |
+                                  ((uint32_t)f32_to_bf16_bits(acc[3] * rw) << 16);
+              *(uint2*)(C + (int64_t)slot_id * p.ldc + g * 16 + 4 * lg) = make_uint2(lo, hi);
+            }
           }
-        } else {
-          if (tok_ok) {
-            const float rw = p.mul_routed ? load_weight_any(p.topk_w, p.topk_w_dtype, slot) : 1.f;
-            const uint32_t lo = (uint32_t)f32_to_bf16_bits(acc[0] * rw) |
-                                ((uint32_t)f32_to_bf16_bits(acc[1] * rw) << 16);
-            const uint32_t hi = (uint32_t)f32_to_bf16_bits(acc[2] * rw) |
-                                ((uint32_t)f32_to_bf16_bits(acc[3] * rw) << 16);
-            *(uint2*)(C + (int64_t)slot * p.ldc + g * 16 + 4 * lg) = make_uint2(lo, hi);
-          }
+          if (!more) return;
+          break;
         }
       }
     }
   };
 
-  if constexpr (TOKENS) {
-    // All token rows (the host checked they fit): one staging, one barrier.
-    const int ntok = (int)((p.M + p.top_k - 1) / p.top_k);
-    if constexpr (STAGE == STAGE_TOKENS_Q16) stage_copy_q16(ntok);
-    else stage_quant(ntok, [&](int r) { return r; });
-    __syncthreads();
-    process(a_first, a_last, 0, 0x7fffffff, 0);
-  } else {
-    // Windows over the CU's experts: as many whole experts as fit in `cap`
-    // rows, or `cap` rows of one larger expert.  Usually a single window.
-    int a = a_first, r = 0;
-    while (a <= a_last) {
-      const int wa0 = a, wr0 = r;
-      int wa1 = a, wr1 = 0x7fffffff, nrows;
-      const int rem = sCnt[sAct[a]] - r;
-      if (rem > cap) {
-        nrows = cap;
-        wr1 = r + cap;
-        r += cap;
-      } else {
-        nrows = rem;
+  // Windows over the CU's experts: as many whole experts as fit in `cap`
+  // rows, or `cap` rows of one larger expert.  Usually a single window.
+  int a = a_first, r = 0;
+  bool first_window = true;
+  while (a <= a_last) {
+    wa0 = a;
+    wr0 = r;
+    wa1 = a;
+    wr1 = 0x7fffffff;
+    int nrows;
+    const int rem = sCnt[sAct[a]] - r;
+    if (rem > cap) {
+      nrows = cap;
+      wr1 = r + cap;
+      r += cap;
+    } else {
+      nrows = rem;
+      ++a;
+      r = 0;
+      while (a <= a_last && nrows + sCnt[sAct[a]] <= cap) {
+        nrows += sCnt[sAct[a]];
+        wa1 = a;
         ++a;
-        r = 0;
-        while (a <= a_last && nrows + sCnt[sAct[a]] <= cap) {
-          nrows += sCnt[sAct[a]];
-          wa1 = a;
-          ++a;
-        }
       }
-      const int lbase = sOff[sAct[wa0]] + wr0;  // list index of staged row 0
-      __syncthreads();                           // the previous window is done with LDS
-      stage_quant(nrows, [&](int j) { return sList[lbase + j] / p.top_k; });
-      __syncthreads();
-      process(wa0, wa1, wr0, wr1, lbase);
     }
+    const int lbase = sOff[sAct[wa0]] + wr0;  // list index of staged row 0
+    if (!first_window) lds_sync();             // every wave is done with the previous window
+    first_window = false;
+    if (w < kCuStageWaves) {
+      const auto arow_of = [&](int j) { return sList[lbase + j] / p.top_k; };
+      if constexpr (STAGE == STAGE_Q16) stage_copy_q16(nrows, arow_of);
+      else stage_quant(nrows, arow_of);
+      if (EPI != EPI_ACT && p.mul_routed)
+        for (int j = tid; j < nrows; j += ST)
+          sRw[j] = load_weight_any(p.topk_w, p.topk_w_dtype, sList[lbase + j]);
+    }
+    lds_sync();
+    run_window(lbase);
   }
+  wait_vmcnt<0>();  // no DMA outlives the kernel
 }
 
 static int g_num_cu = 0;
@@ -671,42 +876,22 @@ static int run_stream_fp8_cu(const GemmArgs& a, int cap, size_t shmem, hipStream
 // does not fit it.
 template <int KS>
 static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, int* status) {
-  const size_t lists = cu_lists_bytes(a.num_experts, a.M);
-  const size_t per_row = (size_t)cu_pitch<KS>() + KS * 4;
-  if (a.top_k > 1) {
-    // Token rows: all of them must fit.
-    const int ntok = (int)((a.M + a.top_k - 1) / a.top_k);
-    const size_t shmem = cu_rows_off<KS>(a.num_experts, a.M, ntok) + (size_t)ntok * cu_pitch<KS>();
-    if (shmem > kCuLdsMax - 1024) return false;
-    int stage;
-    if (a.a_scale && a.a_q16) stage = STAGE_TOKENS_Q16;
-    else if (!a.a_scale) stage = STAGE_TOKENS_H16;
-    else return false;
-    if (stage == STAGE_TOKENS_Q16)
-      *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_TOKENS_Q16>(a, ntok, shmem, stream)
-                               : run_stream_fp8_cu<EPI_STORE, KS, STAGE_TOKENS_Q16>(a, ntok, shmem, stream);
-    else
-      *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_TOKENS_H16>(a, ntok, shmem, stream)
-                               : run_stream_fp8_cu<EPI_STORE, KS, STAGE_TOKENS_H16>(a, ntok, shmem, stream);
-    return true;
-  }
-  if (a.a_scale) return false;  // slot rows are quantised while staged
-  // Slot rows: as many as the LDS budget allows (windows beyond that).
-  const size_t avail = kCuLdsMax - 1024 - lists - 16;
-  int cap = (int)(avail / per_row);
+  const size_t per_row = (size_t)cu_pitch<KS>() + (KS + 1) * 4;
+  if (a.a_scale && !a.a_q16) return false;  // e4m3fn rows: the LDS-staged kernel
+  // Rows staged per window: as many as the LDS budget allows.
+  // 1 KB stays free for the kernel's static LDS.
+  const size_t fixed = cu_sc_off<KS>(a.num_experts, a.M) + 16 + 1024;
+  if (fixed + 4 * per_row > kCuLdsMax) return false;  // windows need a few rows
+  int cap = (int)((kCuLdsMax - fixed) / per_row);
   if (cap > 1024) cap = 1024;
-  if (cap < 16) return false;
   const size_t shmem = cu_rows_off<KS>(a.num_experts, a.M, cap) + (size_t)cap * cu_pitch<KS>();
-  *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_SLOTS_H16>(a, cap, shmem, stream)
-                           : run_stream_fp8_cu<EPI_STORE, KS, STAGE_SLOTS_H16>(a, cap, shmem, stream);
+  if (a.a_q16)
+    *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_Q16>(a, cap, shmem, stream)
+                             : run_stream_fp8_cu<EPI_STORE, KS, STAGE_Q16>(a, cap, shmem, stream);
+  else
+    *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_H16>(a, cap, shmem, stream)
+                             : run_stream_fp8_cu<EPI_STORE, KS, STAGE_H16>(a, cap, shmem, stream);
   return true;
-}
-
-bool stream_fp8_tokens_fit(int64_t tokens, int K, int E, int64_t slots) {
-  if (K % 128 != 0 || K / 128 > 16) return false;
-  const size_t lists = ((size_t)3 * E + (size_t)((slots + 3) & ~3ll)) * 4;
-  const size_t need = lists + (size_t)tokens * (K / 128) * 4 + 16 + (size_t)tokens * (K * 2 + 16);
-  return need <= kCuLdsMax - 1024;
 }
 
 bool stream_fp8_supported(int K, int N, int inter, int epi) {
@@ -756,7 +941,8 @@ int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream
     if (done) return st;
   }
   if (a.a_q16) {
-    set_last_error("stream_fp8: widened activations need the CU-resident kernel (shape too large)");
+    set_last_error("stream_fp8: widened activations need the CU-resident kernel (exact, router ids, "
+                   "at most %lld slots)", (long long)kStreamMaxIdsSlots);
     return kUnsupported;
   }
   switch (a.K / 128) {

@@ -104,14 +104,15 @@ def test_stream_gemm_decode_layer(M, a_mode, ids64):
     assert_moe_close(out, ref, what=f"stream gemm M={M} A={a_mode}")
 
 
-def test_stream_gemm_skewed_routing_uses_windows():
-    """Every token routed to the same 8 experts (128 slots each): the down
-    GEMM's per-CU row set exceeds its LDS budget and is processed in
-    windows; the gate_up GEMM (128 token rows) takes the LDS-staged kernel."""
+@pytest.mark.parametrize("a_mode", ["q16", "bf16"])
+def test_stream_gemm_skewed_routing_uses_windows(a_mode):
+    """Every token routed to the same 8 experts (128 slots each): each CU's
+    staged row set exceeds its LDS budget and is processed in windows."""
     from mstar_amd import _lib, ops
     q1, s1, q2, s2 = _weights()
     M = 128
-    x, _ = _inputs(M, seed=5)
+    x, logits = _inputs(M, seed=5)
+    _, _, hq, hs = _route_quant(x, logits)
     g = torch.Generator().manual_seed(6)
     ti = torch.stack([torch.randperm(8, generator=g) for _ in range(M)]).int()
     tw = torch.softmax(torch.randn(M, K_TOP, generator=g), dim=-1)
@@ -119,24 +120,23 @@ def test_stream_gemm_skewed_routing_uses_windows():
     c2 = torch.empty(slots, I, dtype=torch.bfloat16, device=DEV)
     c3 = torch.empty(slots, H, dtype=torch.bfloat16, device=DEV)
     twd, tid = tw.to(DEV), ti.to(DEV)
-    _stream_gemm(x.to(DEV), _lib.DT_BF16, None, q1, s1, c2, twd, tid, slots, 2 * I, H, K_TOP, 0, 0)
+    if a_mode == "q16":
+        _stream_gemm(hq, _lib.DT_FP8_AS_BF16, hs, q1, s1, c2, twd, tid, slots, 2 * I, H, K_TOP, 0, 0)
+    else:
+        _stream_gemm(x.to(DEV), _lib.DT_BF16, None, q1, s1, c2, twd, tid, slots, 2 * I, H, K_TOP, 0, 0)
     _stream_gemm(c2, _lib.DT_BF16, None, q2, s2, c3, twd, tid, slots, H, I, 1, 1, -1)
     out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
     ops.moe_sum_reduce(c3.view(M, K_TOP, H), out, 1.0)
     ref = _ref(x, tw, ti.long())
-    assert_moe_close(out, ref, what="stream gemm skewed")
+    assert_moe_close(out, ref, what=f"stream gemm skewed A={a_mode}")
 
 
-def test_stream_gemm_rejects_widened_rows_that_do_not_fit():
-    """FP8_AS_BF16 activations need every token row in LDS: 128 rows of
-    2048 do not fit, and the call says so instead of falling back."""
+def test_stream_gemm_rejects_widened_rows_beyond_slot_limit():
+    """FP8_AS_BF16 activations are served by the router-ids kernel only, for
+    at most 1024 slots; beyond that the call says so."""
     from mstar_amd import _lib
-    q1, s1, _, _ = _weights()
-    M = 128
-    hq = torch.zeros(M, H, dtype=torch.bfloat16, device=DEV)
-    hs = torch.ones(M, H // 128, dtype=torch.float32, device=DEV)
-    ti = torch.zeros(M * K_TOP, dtype=torch.int32, device=DEV)
-    tw = torch.ones(M * K_TOP, dtype=torch.float32, device=DEV)
-    c2 = torch.empty(M * K_TOP, I, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(_lib.MstarError, match="widened"):
-        _stream_gemm(hq, _lib.DT_FP8_AS_BF16, hs, q1, s1, c2, tw, ti, M * K_TOP, 2 * I, H, K_TOP, 0, 0)
+    lib = _lib.load()
+    st = lib.mstar_moe_stream_gemm(None, _lib.DT_FP8_AS_BF16, None, None, None, None, None,
+                                   _lib.DT_F32, None, _lib.DT_I32, 2048, E, 2 * I, H, K_TOP, 0, 0,
+                                   None)
+    assert st == 1  # invalid argument: num_slots > 1024
