@@ -142,6 +142,59 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 constexpr uint32_t kOffNone = 0xFFFFFFF0u;  // an offset no buffer here reaches
 
+// ---- DPP reductions (no LDS round trips).  row_ror:n rotates values
+// within each row of 16 lanes; after rotations by 1, 2, 4 and 8 every lane
+// of a row holds the row's reduction (association order differs per lane,
+// so sums are read from one fixed lane per row).
+template <int N>
+__device__ __forceinline__ int dpp_row_ror(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, 0x120 + N, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t row_umax16(uint32_t v) {
+  v = max(v, (uint32_t)dpp_row_ror<1>((int)v));
+  v = max(v, (uint32_t)dpp_row_ror<2>((int)v));
+  v = max(v, (uint32_t)dpp_row_ror<4>((int)v));
+  v = max(v, (uint32_t)dpp_row_ror<8>((int)v));
+  return v;
+}
+__device__ __forceinline__ float row_fmax16(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, dpp_row_ror<1>(__builtin_bit_cast(int, v))));
+  v = fmaxf(v, __builtin_bit_cast(float, dpp_row_ror<2>(__builtin_bit_cast(int, v))));
+  v = fmaxf(v, __builtin_bit_cast(float, dpp_row_ror<4>(__builtin_bit_cast(int, v))));
+  v = fmaxf(v, __builtin_bit_cast(float, dpp_row_ror<8>(__builtin_bit_cast(int, v))));
+  return v;
+}
+__device__ __forceinline__ float row_fsum16(float v) {
+  v += __builtin_bit_cast(float, dpp_row_ror<1>(__builtin_bit_cast(int, v)));
+  v += __builtin_bit_cast(float, dpp_row_ror<2>(__builtin_bit_cast(int, v)));
+  v += __builtin_bit_cast(float, dpp_row_ror<4>(__builtin_bit_cast(int, v)));
+  v += __builtin_bit_cast(float, dpp_row_ror<8>(__builtin_bit_cast(int, v)));
+  return v;
+}
+// Wave-uniform results: the four row results combined in row order.
+__device__ __forceinline__ uint32_t wave_umax_dpp(uint32_t v) {
+  v = row_umax16(v);
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ float wave_fmax_dpp(float v) {
+  v = row_fmax16(v);
+  const int iv = __builtin_bit_cast(int, v);
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48))));
+}
+__device__ __forceinline__ float wave_fsum_dpp(float v) {
+  v = row_fsum16(v);
+  const int iv = __builtin_bit_cast(int, v);
+  return ((__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32))) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+}
+
 // Per-token-group-128 FP8 quantisation of 8 consecutive 16-bit elements
 // (raw: 16 bytes of bf16/fp16 bits); the 16 aligned lanes that hold one
 // 128-element group cooperate on its amax.  s = max(amax, 1e-10) / 448 and
@@ -158,7 +211,7 @@ __device__ __forceinline__ int2 quant_group8(v4i raw, float& scale) {
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-  amax = group_max<16>(amax);
+  amax = row_fmax16(amax);  // the 16 lanes of a group are one DPP row
   const float sc = fmaxf(amax, kQuantEps) / kFp8Max;
   scale = sc;
   return make_int2(cvt_fp8x4(clamp_fp8(f[0] / sc), clamp_fp8(f[1] / sc), clamp_fp8(f[2] / sc),

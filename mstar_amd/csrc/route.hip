@@ -31,91 +31,63 @@ __device__ __forceinline__ uint32_t float_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Inverse of float_key.
+__device__ __forceinline__ float key_float(uint32_t k) {
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 // Softmax top-k of one token by one wave (EPL = experts per lane,
 // ceil(E / 64); expert e sits in lane e % 64, slot e / 64).
 //
-// Selection is a radix select on order-preserving integer keys of the
-// logits (softmax is monotonic, so ranking logits ranks probabilities): 32
-// MSB-first steps, each one ballot + popcount per slot, find the k-th
-// largest key T; keys > T are selected, and of the keys == T the lowest
-// expert indices fill the rest.  Output ranks (value descending, ties by
-// index) come from k scalar broadcasts.  No cross-lane shuffles except the
-// three reductions (max, sum, selected sum) of the softmax.
-// emit(rank, expert, weight) is called once per selected expert.
-// v[j] holds the logit of expert j * 64 + lane (-inf past E).
+// Selection: k rounds of argmax over order-preserving integer keys of the
+// logits (softmax is monotonic, so ranking logits ranks probabilities).
+// Each round is a DPP max over the wave, then a ballot for the lowest
+// expert index holding that key (ties go to the lower index), which is
+// removed for the next round.  Ranks come out in order (value descending,
+// ties by index).  The softmax max and sum are DPP reductions too; nothing
+// goes through LDS.  emit(rank, expert, weight) runs on lane `rank` for
+// each of the k selections (k <= 64).
 template <int EPL, typename Emit>
 __device__ __forceinline__ void topk_wave(const float (&v)[EPL], int E, int k, int renorm, int lane,
                                           const Emit& emit) {
   uint32_t key[EPL];
-  bool valid[EPL];
-  float mx = -INFINITY;
+  float mxl = -INFINITY;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    const int e = j * 64 + lane;
-    valid[j] = e < E;
-    key[j] = valid[j] ? float_key(v[j]) : 0u;
-    mx = fmaxf(mx, v[j]);
+    const bool valid = j * 64 + lane < E;
+    key[j] = valid ? float_key(v[j]) : 0u;  // 0 is below every valid key
+    mxl = fmaxf(mxl, valid ? v[j] : -INFINITY);
   }
-  mx = wave_max(mx);
-  float s = 0.f;
+  const float mx = wave_fmax_dpp(mxl);
+  float sl = 0.f;
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) s += valid[j] ? __expf(v[j] - mx) : 0.f;
-  s = wave_sum(s);
+  for (int j = 0; j < EPL; ++j) sl += j * 64 + lane < E ? __expf(v[j] - mx) : 0.f;
+  const float s = wave_fsum_dpp(sl);
 
-  // ---- radix select of the k-th largest key
-  uint32_t prefix = 0;
-  int need = k;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t hi_mask = 0xFFFFFFFFu << bit;
-    const uint32_t cand = prefix | (1u << bit);
-    int cnt = 0;
+  float my_p = 0.f, psum = 0.f;
+  int my_id = 0;
+  for (int r = 0; r < k; ++r) {
+    uint32_t lm = key[0];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) cnt += __builtin_popcountll(__ballot(valid[j] && (key[j] & hi_mask) == cand));
-    if (cnt >= need) prefix = cand;
-    else need -= cnt;
-  }
-  // ---- selection: keys above T, then `need` ties at T by ascending index
-  const uint64_t lt = (1ull << lane) - 1ull;
-  bool sel[EPL];
-  int ties_before = 0;
+    for (int j = 1; j < EPL; ++j) lm = max(lm, key[j]);
+    const uint32_t m = wave_umax_dpp(lm);
+    int sel = -1;
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const bool eq = valid[j] && key[j] == prefix;
-    const uint64_t beq = __ballot(eq);
-    const int tie_rank = ties_before + __builtin_popcountll(beq & lt);
-    sel[j] = valid[j] && (key[j] > prefix || (eq && tie_rank < need));
-    ties_before += __builtin_popcountll(beq);
-  }
-  // ---- output rank of each selected expert
-  int rank[EPL];
+    for (int j = 0; j < EPL; ++j) {
+      const uint64_t b = __ballot(key[j] == m);
+      if (sel < 0 && b) sel = j * 64 + __builtin_ctzll(b);
+    }
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) rank[j] = 0;
-#pragma unroll
-  for (int j2 = 0; j2 < EPL; ++j2) {
-    uint64_t m = __ballot(sel[j2]);
-    while (m) {
-      const int src = __builtin_ctzll(m);
-      m &= m - 1ull;
-      const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)key[j2], src);
-      const int is = j2 * 64 + src;
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) {
-        const int idx = j * 64 + lane;
-        rank[j] += (ks > key[j] || (ks == key[j] && is < idx)) ? 1 : 0;
-      }
+    for (int j = 0; j < EPL; ++j)
+      if (sel == j * 64 + lane) key[j] = 0u;
+    const float p = __expf(key_float(m) - mx) / s;
+    psum += p;
+    if (lane == r) {
+      my_p = p;
+      my_id = sel;
     }
   }
-  float p[EPL];
-  float psum = 0.f;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    p[j] = sel[j] ? __expf(v[j] - mx) / s : 0.f;
-    psum += p[j];
-  }
-  if (renorm) psum = wave_sum(psum);
-#pragma unroll
-  for (int j = 0; j < EPL; ++j)
-    if (sel[j]) emit(rank[j], j * 64 + lane, renorm ? p[j] / psum : p[j]);
+  if (lane < k) emit(lane, my_id, renorm ? my_p / psum : my_p);
 }
 
 // Top-k of tokens t0, t0 + stride, ... (< t1) by one wave, a batch at a
@@ -149,10 +121,10 @@ __device__ __forceinline__ void topk_tokens(const LT* __restrict__ logits, int64
   }
 }
 
-// One wave per token.  With `hidden`, the wave also quantises the token's
-// bf16 hidden row per group of 128 for the FP8 expert GEMMs that follow (hq
-// [M, H]: the e4m3fn values widened to bf16; hs [M, H/128]): the routing
-// launch carries the activation quantisation for free.
+// One wave per token.  With `hidden`, a second wave per token quantises the
+// token's bf16 hidden row per group of 128 for the FP8 expert GEMMs that
+// follow (hq [M, H]: the e4m3fn values widened to bf16; hs [M, H/128]): the
+// routing launch carries the activation quantisation.
 template <typename LT, int EPL>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict__ logits,
                                                            int64_t M, int E, int k, int renorm,
@@ -163,47 +135,45 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict_
                                                            int64_t H, uint16_t* __restrict__ hq,
                                                            float* __restrict__ hs) {
   const int lane = threadIdx.x & 63;
-  const int64_t tok = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  // With `hidden`, two waves per token: the even one routes, the odd one
+  // quantises the hidden row, in parallel.
+  const int wpt = hidden ? 2 : 1;
+  const int64_t gw = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t tok = gw / wpt;
   if (tok >= M) return;
+  if (wpt == 2 && (gw & 1)) {
+    constexpr int kQB = 4;  // groups of 128 per lane group in flight
+    for (int64_t c0 = 0; c0 < H; c0 += kQB * 512) {
+      v4i raw[kQB];
+#pragma unroll
+      for (int b = 0; b < kQB; ++b) {
+        const int64_t c = c0 + (int64_t)b * 512 + lane * 8;
+        raw[b] = c < H ? *(const v4i*)(hidden + tok * H + c) : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int b = 0; b < kQB; ++b) {
+        const int64_t c = c0 + (int64_t)b * 512 + lane * 8;
+        float sc;
+        const int2 codes = quant_group8<kBF16>(raw[b], sc);
+        if (c < H) {
+          *(v4i*)(hq + tok * H + c) = fp8x8_to_bf16x8_bits(codes.x, codes.y);
+          if ((lane & 15) == 0) hs[tok * (H / 128) + c / 128] = sc;
+        }
+      }
+    }
+    return;
+  }
   float v[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = j * 64 + lane;
     v[j] = e < E ? load_logit<LT>(logits + tok * E, e) : -INFINITY;
   }
-  // Hidden row loads go out with the logits (4 groups of 128 per pass).
-  constexpr int kQB = 4;
-  v4i raw[kQB];
-  if (hidden) {
-#pragma unroll
-    for (int b = 0; b < kQB; ++b) {
-      const int64_t c = (int64_t)b * 512 + lane * 8;
-      raw[b] = c < H ? *(const v4i*)(hidden + tok * H + c) : v4i{0, 0, 0, 0};
-    }
-  }
   topk_wave<EPL>(v, E, k, renorm, lane, [&](int r, int id, float w) {
     w_out[tok * k + r] = w;
     if (ids32) ids32[tok * k + r] = id;
     if (ids64) ids64[tok * k + r] = id;
   });
-  if (!hidden) return;
-  for (int64_t c0 = 0; c0 < H; c0 += kQB * 512) {
-#pragma unroll
-    for (int b = 0; b < kQB; ++b) {
-      const int64_t c = c0 + (int64_t)b * 512 + lane * 8;
-      if (c0 > 0) raw[b] = c < H ? *(const v4i*)(hidden + tok * H + c) : v4i{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int b = 0; b < kQB; ++b) {
-      const int64_t c = c0 + (int64_t)b * 512 + lane * 8;
-      float sc;
-      const int2 codes = quant_group8<kBF16>(raw[b], sc);
-      if (c < H) {
-        *(v4i*)(hq + tok * H + c) = fp8x8_to_bf16x8_bits(codes.x, codes.y);
-        if ((lane & 15) == 0) hs[tok * (H / 128) + c / 128] = sc;
-      }
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -526,8 +496,9 @@ int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, 
   // One wave per token.  Small batches get one-wave workgroups, so the
   // tokens spread over as many CUs as possible (the radix select is a long
   // dependent chain; one SIMD per token keeps it at issue latency).
-  const int wpb = M <= 2048 ? 1 : 4;
-  dim3 grid((unsigned)((M + wpb - 1) / wpb)), block(64 * wpb);
+  const int tpb = M <= 2048 ? 1 : 4;         // tokens per workgroup
+  const int wpt = hidden ? 2 : 1;              // waves per token
+  dim3 grid((unsigned)((M + tpb - 1) / tpb)), block(64 * tpb * wpt);
   const int epl = (E + 63) / 64;
 #define MSTAR_TOPK_CASE(N)                                                                   \
   case N:                                                                                    \

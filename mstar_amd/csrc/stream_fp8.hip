@@ -368,7 +368,6 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
 enum : int { STAGE_Q16 = 0, STAGE_H16 = 1 };
 constexpr int kCuThreads = 512;
 constexpr int kCuWaves = kCuThreads / 64;
-constexpr int kCuStageWaves = 2;  // waves that stage rows; the others prefetch weights meanwhile
 constexpr int kCuRing = 3;        // ring slots per wave
 constexpr size_t kCuLdsMax = 160 * 1024;
 constexpr int kDmaAux = 2;        // cache policy of the weight stream (streaming)
@@ -403,6 +402,8 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   constexpr int SLOT = KC * 2048;     // ring slot bytes
   constexpr int DPC = 2 * KC;         // DMA instructions per chunk
   constexpr int SPT = (int)(kStreamMaxIdsSlots / kCuThreads);  // router ids per thread
+  // Waves that stage activation rows; the others prefetch weights meanwhile.
+  constexpr int SW = STAGE == STAGE_Q16 ? 2 : 4;
   typedef __attribute__((address_space(3))) void* lds_void_ptr;
   extern __shared__ __align__(16) uint8_t smem[];
   const int E = p.num_experts;
@@ -493,7 +494,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   // ---- prefetch: waves that do not stage start their first item's weights
   // now; lds_sync leaves the DMA in flight through the rest of the prologue.
   const int it_first = i0 + w;
-  const bool prefetched = w >= kCuStageWaves && it_first < i1;
+  const bool prefetched = w >= SW && it_first < i1;
   if (prefetched) {
     const int a = it_first / IPE;
     const uint8_t *s0, *s1;
@@ -529,33 +530,46 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   lds_sync();
   const int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
 
-  // ---- staging (waves < kCuStageWaves): `nrows` rows; row j reads A row arow_of(j).
-  constexpr int ST = kCuStageWaves * 64;
+  // ---- staging (waves < SW): `nrows` rows; row j reads A row arow_of(j).
+  // The staging waves hold no prefetched weights, so their loads are all in
+  // flight at once and one wait covers them.
+  constexpr int ST = SW * 64;
   auto stage_copy_q16 = [&](int nrows, auto arow_of) {
-    constexpr int PPR = KS * 16;  // 16-byte pieces per row
-    const int pieces = nrows * PPR;
-    for (int base = 0; base < pieces; base += ST * 4) {
-      v4i v[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int pc = base + j * ST + tid;
-        const int r = pc / PPR, c = pc - r * PPR;
-        v[j] = pc < pieces ? *(const v4i*)(A16 + (int64_t)arow_of(r) * p.lda + c * 8) : v4i{0, 0, 0, 0};
+    if constexpr (KS % 4 == 0) {
+      // LDS-DMA: 1 KB (64 lanes x 16 bytes) of one row per instruction.
+      constexpr int CPR = KS / 4;  // 1 KB pieces per row
+      for (int pc = w; pc < nrows * CPR; pc += SW) {
+        const int r = pc / CPR, c = pc - r * CPR;
+        __builtin_amdgcn_global_load_lds((const void*)(A16 + (int64_t)arow_of(r) * p.lda + c * 512 + lane * 8),
+                                         (lds_void_ptr)(sRows + r * PITCH + c * 1024), 16, 0, 0);
       }
+    } else {
+      constexpr int PPR = KS * 16;  // 16-byte pieces per row
+      const int pieces = nrows * PPR;
+      for (int base = 0; base < pieces; base += ST * 8) {
+        v4i v[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int pc = base + j * ST + tid;
-        const int r = pc / PPR, c = pc - r * PPR;
-        if (pc < pieces) *(v4i*)(sRows + r * PITCH + c * 16) = v[j];
+        for (int j = 0; j < 8; ++j) {
+          const int pc = base + j * ST + tid;
+          const int r = pc / PPR, c = pc - r * PPR;
+          v[j] = pc < pieces ? *(const v4i*)(A16 + (int64_t)arow_of(r) * p.lda + c * 8) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int pc = base + j * ST + tid;
+          const int r = pc / PPR, c = pc - r * PPR;
+          if (pc < pieces) *(v4i*)(sRows + r * PITCH + c * 16) = v[j];
+        }
       }
     }
     for (int i = tid; i < nrows * KS; i += ST) {
       const int r = i / KS, ks = i - r * KS;
       sSc[i] = p.a_scale[(int64_t)arow_of(r) * p.ld_as + ks];
     }
+    wait_vmcnt<0>();
   };
   auto stage_quant = [&](int nrows, auto arow_of) {
-    constexpr int B = 2;
+    constexpr int B = 8;
     const int groups = nrows * KS;
     for (int g0 = 0; g0 < groups; g0 += (ST / 16) * B) {
       v4i raw[B];
@@ -800,7 +814,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
     const int lbase = sOff[sAct[wa0]] + wr0;  // list index of staged row 0
     if (!first_window) lds_sync();             // every wave is done with the previous window
     first_window = false;
-    if (w < kCuStageWaves) {
+    if (w < SW) {
       const auto arow_of = [&](int j) { return sList[lbase + j] / p.top_k; };
       if constexpr (STAGE == STAGE_Q16) stage_copy_q16(nrows, arow_of);
       else stage_quant(nrows, arow_of);
