@@ -37,11 +37,10 @@ constexpr float kFp8Max = 448.0f;
 constexpr float kQuantEps = 1e-10f;
 
 // bf16 <-> f32 with round-to-nearest-even, matching torch's float->bfloat16.
-__device__ __host__ inline uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+// Round to nearest even (NaN stays NaN): the hardware conversion
+// (v_cvt_pk_bf16_f32 on gfx950).
+__device__ inline uint16_t f32_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __host__ inline float bf16_bits_to_f32(uint16_t b) {
   return __builtin_bit_cast(float, (uint32_t)b << 16);
@@ -268,11 +267,13 @@ __device__ inline float load_weight_any(const void* w, int dtype, int64_t i) {
   return dtype == kBF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
 }
 
-__device__ inline float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
+// x * sigmoid(x) with the hardware reciprocal (about 1 ulp); the callers
+// round the result to bf16.
+__device__ inline float silu_f32(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ inline float gelu_tanh_f32(float x) {
   const float k = 0.7978845608028654f;
   float t = k * (x + 0.044715f * x * x * x);
-  float th = 2.0f / (1.0f + __expf(-2.0f * t)) - 1.0f;
+  float th = 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * t)) - 1.0f;
   return 0.5f * x * (1.0f + th);
 }
 template <int ACT>
