@@ -1,30 +1,32 @@
 // Large-tile FP8 GEMM for prefill-sized MoE layers and the dense W8A8 GEMM.
 //
 // Persistent: one 512-thread workgroup (8 waves, 4 x 2) per CU walks output
-// tiles of 256 (tokens) x 128 (weight rows) in rounds of one tile per
+// tiles of 256 (tokens) x 256 (weight rows) in rounds of one tile per
 // workgroup; within a round the 32 workgroups of an XCD take 32 consecutive
 // tiles, so the n-tiles of an m-block (which share A rows) and neighbouring
 // m-blocks of an expert (which share weights) meet in the same L2.  K is
 // walked in 128-wide steps -- exactly one FP8 scale block per step.
 //
-// Data movement.  A step's operands (32 KB of activations, 16 KB of weights
+// Data movement.  A step's operands (32 KB of activations, 32 KB of weights
 // and, when block-scaled, the step's activation and weight scales) go
 // straight from global memory into LDS with LDS-DMA loads
-// (global_load_lds_dwordx4: lane l's bytes land at base + 16 l), into a ring
-// of three stages.  The DMA cursor runs two steps ahead of the math across
-// tile boundaries, so the next tile's first steps load while the current
-// tile's epilogue stores its results; the tile metadata (sorted_ids) arrives
+// (global_load_lds_dwordx4: lane l's bytes land at base + 16 l), into two
+// stages: the square tile halves the L2->LDS bytes per MFMA flop of a
+// 256 x 128 tile, which is what bounds this loop.  The DMA cursor runs one
+// step ahead of the math across tile boundaries, so the next tile's first
+// step loads while the current tile's epilogue stores its results; the tile metadata (sorted_ids) arrives
 // the same way, into three rotating LDS buffers.  Rows are 128 bytes with
 // the 16-byte chunks XOR-swizzled by (row & 7), so the lanes of a
 // ds_read_b128 phase hit distinct banks.  One barrier per step.
 //
-// Math.  Each wave owns a 64 x 64 sub-tile as 2 x 2 tiles of 32 x 32, two
-// chained v_mfma_f32_32x32x64_f8f6f4 per tile per step.  The product is
-// computed transposed (weights as the MFMA's A operand, tokens as B) so that
-// each lane holds one token column: with block-scaled operands (MoE) a
-// step's partial is promoted with one factor s_a[token, kb] * s_w[block, kb]
-// per lane -- 16 FMAs per tile per step, software-pipelined behind the next
-// tile's MFMAs.  Per-token x per-channel operands (dense): the MFMAs chain
+// Math.  Each wave owns 64 tokens x 128 weight rows as 2 x 4 tiles of
+// 32 x 32, two chained v_mfma_f32_32x32x64_f8f6f4 per tile per step.  The
+// product is computed transposed (weights as the MFMA's A operand, tokens as
+// B) so that each lane holds one token column: with block-scaled operands
+// (MoE) a step's partial is promoted with one factor s_a[token, kb] *
+// s_w[block, kb] per lane -- 16 FMAs per tile per step, overlapped with the
+// MFMAs of the SIMD's other wave (the 128 accumulators leave no registers
+// for a second product in flight).  Per-token x per-channel operands (dense): the MFMAs chain
 // into the accumulator and the scales are applied in the epilogue.
 //
 // Grouped mode follows the reference's fused_moe_kernel contract
@@ -36,11 +38,11 @@
 
 namespace mstar {
 
-constexpr int kBigBM = 256, kBigBN = 128;
-constexpr int kBigWM = 4, kBigWN = 2;  // wave grid; wave tile 64 x 64
-constexpr int kBigStages = 3;
+constexpr int kBigBM = 256, kBigBN = 256;
+constexpr int kBigWM = 4, kBigWN = 2;  // wave grid; wave tile 64 tokens x 128 weight rows
+constexpr int kBigStages = 2;
 // Stage: A tile, B tile (128-byte rows), A-row scales [256], weight-block
-// scales [64] (4 used: one per (wave column, 32-row tile)).
+// scales [64] (8 used: one per (wave column, 32-row tile)).
 constexpr int kBigAsOff = (kBigBM + kBigBN) * 128;
 constexpr int kBigBsOff = kBigAsOff + kBigBM * 4;
 constexpr int kBigStageBytes = kBigBsOff + 64 * 4;
@@ -66,7 +68,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   constexpr int BM = kBigBM, BN = kBigBN, WN = kBigWN, WTM = BM / kBigWM, WTN = BN / kBigWN;
   constexpr int MB = WTM / 32, NB = WTN / 32;      // 32x32 MFMA tiles per wave
   constexpr int AI = BM / 8 / 8, BI = BN / 8 / 8;  // 1 KB DMA instructions per wave per step
-  static_assert(EPI != EPI_ACT || NB == 2, "fused activation pairs one gate and one up tile");
+  static_assert(EPI != EPI_ACT || NB % 2 == 0, "fused activation pairs gate and up tiles");
   static_assert(WN * NB <= 64, "weight-scale slots");
   extern __shared__ __align__(16) uint8_t smem[];
   int* sMeta = (int*)(smem + (size_t)kBigStages * kBigStageBytes);  // [3][kBigMetaInts]
@@ -132,8 +134,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     if constexpr (GROUPED) expert = __builtin_amdgcn_readfirstlane(((const_iptr)p.expert_ids)[mb]);
     b_base = (const uint8_t*)p.B + (int64_t)expert * p.b_estride;
     // Weight row of B-tile row rho; -1 past the edge.  With the fused
-    // activation each wave column's 64 rows are 32 gate rows then the
-    // matching 32 up rows.
+    // activation each wave column's 128 rows are 64 gate rows then the
+    // matching 64 up rows.
     auto brow_of = [&](int rho) -> int {
       if constexpr (EPI == EPI_ACT) {
         const int ww = rho / WTN, q = rho % WTN;
@@ -158,13 +160,13 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     }
     // Scales ride the same DMA stream.  Waves 0-3 move the 256 A-row
     // scales, wave 4 the weight-block scales: lane l the block of (wave
-    // column (l/2) % WN, tile l % 2).
+    // column (l / NB) % WN, 32-row tile l % NB).
     if constexpr (BLOCKSCALE) {
       if (wave < 4) {
         const int s = slot_of(t, buf, wave * 64 + lane);
         sc_src = p.a_scale + (int64_t)(s >= 0 ? s / p.top_k : 0) * p.ld_as;
       } else if (wave == 4) {
-        const int ww = (lane >> 1) % WN, j = lane & 1;
+        const int ww = (lane / NB) % WN, j = lane % NB;
         const int r = brow_of(ww * WTN + j * 32);
         sc_src = (const float*)p.b_scale + (int64_t)expert * p.bs_estride +
                  (int64_t)(r < 0 ? 0 : r / 128) * p.bs_ld;
@@ -186,41 +188,48 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
         const int s = slot_of(t, buf, wave * 64 + lane);
         __builtin_amdgcn_global_load_lds((const void*)(p.a_scale + (s >= 0 ? s : 0)),
                                          (lds_void_ptr)(meta + BM + wave * 64), 4, 0, 0);
-      } else if (wave < 6) {
+      } else {
         const int c = nt * BN + (wave - 4) * 64 + lane;
         __builtin_amdgcn_global_load_lds((const void*)((const float*)p.b_scale + (c < p.N ? c : 0)),
                                          (lds_void_ptr)(meta + 2 * BM + (wave - 4) * 64), 4, 0, 0);
       }
     }
   };
-  auto issue_step = [&](int kb, int stage) {
+  // DMA instruction n of step kb into ring stage `stage`: n < AI moves A
+  // rows, then BI instructions of B rows; the scales ride with n == 0.
+  auto issue_part = [&](int n, int kb, int stage) {
     uint8_t* st = smem + stage * kBigStageBytes;
-#pragma unroll
-    for (int q = 0; q < AI; ++q)
-      __builtin_amdgcn_global_load_lds((const void*)(a_base + a_off[q] + kb * 128),
-                                       (lds_void_ptr)(st + (wave * (BM / 8) + q * 8) * 128), 16, 0, 0);
-#pragma unroll
-    for (int q = 0; q < BI; ++q)
+    if (n < AI) {
+      __builtin_amdgcn_global_load_lds((const void*)(a_base + a_off[n] + kb * 128),
+                                       (lds_void_ptr)(st + (wave * (BM / 8) + n * 8) * 128), 16, 0, 0);
+    } else {
+      const int q = n - AI;
       __builtin_amdgcn_global_load_lds((const void*)(b_base + b_off[q] + kb * 128),
                                        (lds_void_ptr)(st + BM * 128 + (wave * (BN / 8) + q * 8) * 128),
                                        16, 0, 0);
+    }
     if constexpr (BLOCKSCALE) {
-      if (wave < 4)
-        __builtin_amdgcn_global_load_lds((const void*)(sc_src + kb),
-                                         (lds_void_ptr)(st + kBigAsOff + wave * 256), 4, 0, 0);
-      else if (wave == 4)
-        __builtin_amdgcn_global_load_lds((const void*)(sc_src + kb), (lds_void_ptr)(st + kBigBsOff),
-                                         4, 0, 0);
+      if (n == 0) {
+        if (wave < 4)
+          __builtin_amdgcn_global_load_lds((const void*)(sc_src + kb),
+                                           (lds_void_ptr)(st + kBigAsOff + wave * 256), 4, 0, 0);
+        else if (wave == 4)
+          __builtin_amdgcn_global_load_lds((const void*)(sc_src + kb), (lds_void_ptr)(st + kBigBsOff),
+                                           4, 0, 0);
+      }
     }
   };
-  // DMA instructions per step of this wave (the wait count below).
-  constexpr int kPer = AI + BI;
-  const bool extra = BLOCKSCALE && wave < 5;
+  constexpr int kParts = AI + BI;
+  static_assert(kParts == MB * NB, "one DMA instruction per 32x32 tile of the step");
 
-  // ---- cursor: tile round ji, step ki, global step qi (ring stage qi % 3).
-  int ji = 0, ki = 0, qi = 0;
+  // ---- cursor: tile round ji, step ki, global step qi (ring stage qi % 2).
+  // advance() moves it to the next step (set-up of a new tile included) and
+  // records that step in (ik, ist); past the last step it leaves (ik, ist)
+  // naming a valid address, and the parts issued then load into the stage
+  // nobody reads again.
+  int ji = 0, ki = 0, qi = 0, ik = 0, ist = 0;
   bool more = true;  // the cursor has steps left
-  auto issue_next = [&]() {
+  auto advance = [&]() {
     if (!more) return;
     if (ki == KB) {
       ++ji;
@@ -228,6 +237,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
       const int t = tile_of(ji);
       if (t >= total) {
         more = false;
+        ist = qi % kBigStages;
         return;
       }
       if (KB < 2) {  // metadata of this tile was issued one step ago: let it land
@@ -237,19 +247,21 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
       setup_issue(t, ji % kBigIdBufs);
       issue_ids(tile_of(ji + 1), (ji + 1) % kBigIdBufs);
     }
-    issue_step(ki, qi % kBigStages);
+    ik = ki;
+    ist = qi % kBigStages;
     ++ki;
     ++qi;
   };
 
-  // Prologue: metadata of the first tile, then of the second, then two steps.
+  // Prologue: metadata of the first tile, then of the second, then a step.
   issue_ids(tile_of(0), 0);
   wait_vmcnt<0>();
   __syncthreads();
   setup_issue(tile_of(0), 0);
   issue_ids(tile_of(1), 1);
-  issue_next();
-  issue_next();
+  advance();
+#pragma unroll
+  for (int n = 0; n < kParts; ++n) issue_part(n, ik, ist);
 
   for (int j = 0; tile_of(j) < total; ++j) {
     const int t = tile_of(j);
@@ -261,95 +273,73 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     for (int i = 0; i < MB; ++i)
 #pragma unroll
       for (int jj = 0; jj < NB; ++jj) acc[i][jj] = v16f{};
-    v16f tp[NB];
-    float fp[NB];
-#pragma unroll
-    for (int jj = 0; jj < NB; ++jj) { tp[jj] = v16f{}; fp[jj] = 0.f; }
-    auto promote8 = [&](int i, int jj, int half) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        acc[i][jj][half * 8 + e] = __builtin_fmaf(tp[jj][half * 8 + e], fp[jj], acc[i][jj][half * 8 + e]);
-    };
-    auto fence_sched = [] { __builtin_amdgcn_sched_barrier(0); };
 
     for (int kb = 0; kb < KB; ++kb) {
       const int q = j * KB + kb;  // global step of this computation
-      // Wait for this step's DMA, leaving the next step's in flight.
-      if (qi > q + 1) {
-        if (extra) wait_vmcnt<kPer + 1>();
-        else wait_vmcnt<kPer>();
-      } else {
-        wait_vmcnt<0>();
-      }
+      // Step q is the only one in flight: wait for it.
+      wait_vmcnt<0>();
       // Step q has landed for every wave, and every wave is past step q-1,
       // whose stage the next issue overwrites.
       lds_barrier();
-      issue_next();
+      // The next step's DMA goes out one instruction per 32x32 tile, between
+      // the MFMAs: issued in a burst, the instructions back up in the CU's
+      // address queue and hold the wave at issue.
+      advance();
       const uint8_t* st = smem + (q % kBigStages) * kBigStageBytes;
       const uint8_t* sA = st;
       const uint8_t* sB = st + BM * 128;
-      v8i wf[NB][2];
+      // Token fragments of both row tiles stay in registers for the step;
+      // weight fragments stream one 32-row tile at a time.
+      v8i x[MB][2];
 #pragma unroll
-      for (int jj = 0; jj < NB; ++jj) {
-        const int r = wn * WTN + jj * 32 + l32;
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) wf[jj][kh] = lds_frag_swz(sB + r * 128, r, kh * 4 + lh * 2);
+      for (int i = 0; i < MB; ++i) {
+        const int r = wm * WTM + i * 32 + l32;
+        x[i][0] = lds_frag_swz(sA + r * 128, r, lh * 2);
+        x[i][1] = lds_frag_swz(sA + r * 128, r, 4 + lh * 2);
       }
+      auto load_w = [&](int jj, v8i (&w)[2]) {
+        const int r = wn * WTN + jj * 32 + l32;
+        w[0] = lds_frag_swz(sB + r * 128, r, lh * 2);
+        w[1] = lds_frag_swz(sB + r * 128, r, 4 + lh * 2);
+      };
+      v8i wf[1][2];
+      load_w(0, wf[0]);  // one weight tile at a time (register budget)
       if constexpr (BLOCKSCALE) {
-        float sw[NB];
+        float sa[MB], sw[NB];
 #pragma unroll
-        for (int jj = 0; jj < NB; ++jj) sw[jj] = ((const float*)(st + kBigBsOff))[wn * 2 + jj];
-        v8i x[2][2];
-        float sa[2];
-        auto load_x = [&](int i) {
-          const int r = wm * WTM + i * 32 + l32;
-          x[i & 1][0] = lds_frag_swz(sA + r * 128, r, lh * 2);
-          x[i & 1][1] = lds_frag_swz(sA + r * 128, r, 4 + lh * 2);
-          sa[i & 1] = ((const float*)(st + kBigAsOff))[r];  // this lane's token
-        };
-        load_x(0);
+        for (int i = 0; i < MB; ++i) sa[i] = ((const float*)(st + kBigAsOff))[wm * WTM + i * 32 + l32];
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
-          // Promote the previous row tile (of this step, or the last of the
-          // previous step) while these MFMAs run.
-          const int ip = i == 0 ? MB - 1 : i - 1;
-          const v8i* xi = x[i & 1];
-          v16f tt[NB];
-          fence_sched();
-          tt[0] = mfma_fp8_32x32x64(wf[0][0], xi[0], v16f{});
-          if (i + 1 < MB) load_x(i + 1);
-          promote8(ip, 0, 0);
-          fence_sched();
-          tt[1] = mfma_fp8_32x32x64(wf[1][0], xi[0], v16f{});
-          promote8(ip, 0, 1);
-          fence_sched();
-          tt[0] = mfma_fp8_32x32x64(wf[0][1], xi[1], tt[0]);
-          promote8(ip, 1, 0);
-          fence_sched();
-          tt[1] = mfma_fp8_32x32x64(wf[1][1], xi[1], tt[1]);
-          promote8(ip, 1, 1);
-          fence_sched();
+        for (int jj = 0; jj < NB; ++jj) sw[jj] = ((const float*)(st + kBigBsOff))[wn * NB + jj];
+        // Tiles in order (jj, i); each product is promoted as soon as its
+        // two MFMAs retire (the SIMD's other wave fills the MFMA pipe).
 #pragma unroll
-          for (int jj = 0; jj < NB; ++jj) { tp[jj] = tt[jj]; fp[jj] = sa[i & 1] * sw[jj]; }
+        for (int jj = 0; jj < NB; ++jj) {
+          const v8i* w = wf[0];
+#pragma unroll
+          for (int i = 0; i < MB; ++i) {
+            v16f tt = mfma_fp8_32x32x64(w[0], x[i][0], v16f{});
+            tt = mfma_fp8_32x32x64(w[1], x[i][1], tt);
+            if (i == MB - 1 && jj + 1 < NB) load_w(jj + 1, wf[0]);
+            issue_part(jj * MB + i, ik, ist);
+            const float f = sa[i] * sw[jj];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][jj][e] = __builtin_fmaf(tt[e], f, acc[i][jj][e]);
+          }
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
-          const int r = wm * WTM + i * 32 + l32;
-          const v8i x0 = lds_frag_swz(sA + r * 128, r, lh * 2);
-          const v8i x1 = lds_frag_swz(sA + r * 128, r, 4 + lh * 2);
+        for (int jj = 0; jj < NB; ++jj) {
+          const v8i* w = wf[0];
 #pragma unroll
-          for (int jj = 0; jj < NB; ++jj) acc[i][jj] = mfma_fp8_32x32x64(wf[jj][0], x0, acc[i][jj]);
+          for (int i = 0; i < MB; ++i) acc[i][jj] = mfma_fp8_32x32x64(w[0], x[i][0], acc[i][jj]);
 #pragma unroll
-          for (int jj = 0; jj < NB; ++jj) acc[i][jj] = mfma_fp8_32x32x64(wf[jj][1], x1, acc[i][jj]);
+          for (int i = 0; i < MB; ++i) {
+            acc[i][jj] = mfma_fp8_32x32x64(w[1], x[i][1], acc[i][jj]);
+            issue_part(jj * MB + i, ik, ist);
+          }
+          if (jj + 1 < NB) load_w(jj + 1, wf[0]);
         }
       }
-    }
-    if constexpr (BLOCKSCALE) {
-      // The last step's last row tile (its first step promoted the zero tp
-      // of the tile start, which adds nothing).
-#pragma unroll
-      for (int jj = 0; jj < NB; ++jj) { promote8(MB - 1, jj, 0); promote8(MB - 1, jj, 1); }
     }
 
     // ---- epilogue, straight from registers (the ring keeps loading the
@@ -363,8 +353,9 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
       uint16_t* crow = C + (int64_t)slot * p.ldc;
       if constexpr (EPI == EPI_ACT) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int gcol = nt * (BN / 2) + wn * (WTN / 2) + 8 * q + 4 * lh;
+        for (int jq = 0; jq < NB / 2 * 4; ++jq) {
+          const int jj = jq / 4, q = jq % 4;
+          const int gcol = nt * (BN / 2) + wn * (WTN / 2) + jj * 32 + 8 * q + 4 * lh;
           if (gcol >= p.inter) continue;
           uint32_t packed[2];
 #pragma unroll
@@ -373,8 +364,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
               const int r = 4 * q + 2 * h + e;
-              const float g = round_bf16(acc[i][0][r]);
-              const float u = round_bf16(acc[i][1][r]);
+              const float g = round_bf16(acc[i][jj][r]);
+              const float u = round_bf16(acc[i][jj + NB / 2][r]);
               const float a = round_bf16(p.activation == 0 ? act_f32<0>(g) : act_f32<1>(g));
               two |= (uint32_t)f32_to_bf16_bits(a * u) << (16 * e);
             }
