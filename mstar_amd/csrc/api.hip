@@ -104,7 +104,12 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->off_c2 = take((size_t)pl->slots * I * 2);
   pl->off_c3 = reduce ? take((size_t)pl->slots * H * 2) : 0;
   const bool fp8_tiled = quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream;
-  pl->route_quant = with_route && pl->ids_mode && H % 512 == 0;
+  // With the router in the plan, the routing launch quantises the hidden
+  // rows: widened to bf16 for the router-ids streaming kernel, as e4m3fn
+  // codes for the tiled FP8 GEMM (multi-workgroup routing only).
+  pl->route_quant = with_route && ((pl->ids_mode && H % 512 == 0) ||
+                                   (quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream &&
+                                    route_is_grid(M, top_k)));
   pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;
   pl->off_hs = fp8_tiled || pl->route_quant ? take((size_t)M * (H / 128) * 4) : 0;
   pl->off_cq = fp8_tiled ? take((size_t)pl->slots * I) : 0;
@@ -197,13 +202,21 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
     float* hs = (float*)(ws + pl.off_hs);
     uint8_t* cq = ws + pl.off_cq;
     float* cs = (float*)(ws + pl.off_cs);
-    st = launch_quant_fp8_group(hidden, act_dtype, M, H, H, hq, hs, stream);
-    if (st != kOk) return st;
+    if (!pl.route_quant) {  // else the routing launch wrote hq / hs
+      st = launch_quant_fp8_group(hidden, act_dtype, M, H, H, hq, hs, stream);
+      if (st != kOk) return st;
+    }
     g1.A = hq; g1.lda = H; g1.a_scale = hs; g1.ld_as = H / 128;
+    // The 256-row kernel quantises the activation output in its epilogue;
+    // the smaller tiles store bf16 and a quantisation launch follows.
+    const bool fused_q = pl.bm == kBigBlockM;
+    if (fused_q) { g1.cq = cq; g1.cs = cs; }
     st = launch_tile_gemm(g1, A_FP8G, B_FP8BLK, EPI_ACT, act_dtype, true, pl.bm, stream);
     if (st != kOk) return st;
-    st = launch_quant_fp8_group(cache2, act_dtype, pl.slots, I, I, cq, cs, stream);
-    if (st != kOk) return st;
+    if (!fused_q) {
+      st = launch_quant_fp8_group(cache2, act_dtype, pl.slots, I, I, cq, cs, stream);
+      if (st != kOk) return st;
+    }
     g2.A = cq; g2.lda = I; g2.a_scale = cs; g2.ld_as = I / 128;
     st = launch_tile_gemm(g2, A_FP8G, B_FP8BLK, EPI_STORE, act_dtype, true, pl.bm, stream);
     if (st != kOk) return st;
@@ -524,7 +537,9 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
                       ids32, topk_ids_out, pl.bm, (int32_t*)(ws + pl.off_sorted),
                       (int32_t*)(ws + pl.off_eids), (int32_t*)(ws + pl.off_ntpp), pl.max_padded,
                       (int32_t*)(ws + pl.off_eoff), (int32_t*)(ws + pl.off_ecnt),
-                      ws + pl.off_scratch, pl.scratch_bytes, stream);
+                      ws + pl.off_scratch, pl.scratch_bytes, stream,
+                      pl.route_quant ? hidden : nullptr, hidden_size, ws + pl.off_hq,
+                      (float*)(ws + pl.off_hs));
   if (st != kOk) return st;
   return run_experts(pl, hidden, act_dtype, num_tokens, hidden_size, w1, w2, num_experts, inter,
                      quant, w1_scale, w2_scale, tw, kF32, ids32, kI32, top_k, activation, 1, out,

@@ -33,6 +33,8 @@
 // (mstar/utils/fused_moe/kernels.py:83-138): one 256-row block of
 // `sorted_ids` per tile row, A row = slot / top_k, padding masked, blocks past
 // num_tokens_post_padded are not visited.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -51,7 +53,9 @@ constexpr int kBigStageBytes = kBigBsOff + 64 * 4;
 // (dense weight scales).
 constexpr int kBigMetaInts = 2 * kBigBM + kBigBN;
 constexpr int kBigIdBufs = 3;
-constexpr size_t kBigLds = (size_t)kBigStages * kBigStageBytes + (size_t)kBigIdBufs * kBigMetaInts * 4;
+// Per-token amax exchange between the two wave columns (fused quantisation).
+constexpr size_t kBigRedOff = (size_t)kBigStages * kBigStageBytes + (size_t)kBigIdBufs * kBigMetaInts * 4;
+constexpr size_t kBigLds = kBigRedOff + (size_t)kBigWN * kBigBM * 4;
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
@@ -346,39 +350,100 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     // next tile).  Lane (l32, lh), register e of tile (i, jj): token row
     // wm*WTM + i*32 + l32, weight column wn*WTN + jj*32 + 8*(e/4) + 4*lh + (e%4).
     uint16_t* C = (uint16_t*)p.C;
+    if constexpr (EPI == EPI_ACT) {
+      // a = bf16(bf16(act(bf16(gate))) * bf16(up)): the values the
+      // reference's act_and_mul writes (kernels.py:279-298).
+      float av[MB][NB / 2][16];
+      auto act_all = [&](auto act) {
+        constexpr int A = decltype(act)::value;
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      const int slot = slot_of(t, buf, wm * WTM + i * 32 + l32);
-      if (slot < 0) continue;
-      uint16_t* crow = C + (int64_t)slot * p.ldc;
-      if constexpr (EPI == EPI_ACT) {
+        for (int i = 0; i < MB; ++i)
 #pragma unroll
-        for (int jq = 0; jq < NB / 2 * 4; ++jq) {
-          const int jj = jq / 4, q = jq % 4;
-          const int gcol = nt * (BN / 2) + wn * (WTN / 2) + jj * 32 + 8 * q + 4 * lh;
-          if (gcol >= p.inter) continue;
-          uint32_t packed[2];
+          for (int jj = 0; jj < NB / 2; ++jj)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            uint32_t two = 0;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const int r = 4 * q + 2 * h + e;
+            for (int r = 0; r < 16; ++r) {
               const float g = round_bf16(acc[i][jj][r]);
               const float u = round_bf16(acc[i][jj + NB / 2][r]);
-              const float a = round_bf16(p.activation == 0 ? act_f32<0>(g) : act_f32<1>(g));
-              two |= (uint32_t)f32_to_bf16_bits(a * u) << (16 * e);
+              av[i][jj][r] = round_bf16(round_bf16(act_f32<A>(g)) * u);
             }
-            packed[h] = two;
+      };
+      if (p.activation == 0) act_all(std::integral_constant<int, 0>{});
+      else act_all(std::integral_constant<int, 1>{});
+      if (p.cq) {
+        // Quantise per token and group of 128 columns -- exactly this
+        // tile's columns: amax over the lane pair (lh) and the wave columns
+        // (through LDS), scale = max(amax, eps) / 448, codes = a / scale
+        // rounded to e4m3fn.  The quotient is a * (1/scale) corrected by one
+        // FMA residual step, which rounds like the IEEE division.
+        float* sAmax = (float*)(smem + kBigRedOff);  // [WN][BM]
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          float m = 0.f;
+#pragma unroll
+          for (int jj = 0; jj < NB / 2; ++jj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(av[i][jj][r]));
+          m = fmaxf(m, __shfl_xor(m, 32));
+          if (lh == 0) sAmax[wn * BM + wm * WTM + i * 32 + l32] = m;
+        }
+        lds_sync();
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          const int row = wm * WTM + i * 32 + l32;
+          const int slot = slot_of(t, buf, row);
+          float m = sAmax[row];
+#pragma unroll
+          for (int ww = 1; ww < WN; ++ww) m = fmaxf(m, sAmax[ww * BM + row]);
+          const float sc = fmaxf(m, kQuantEps) / kFp8Max;
+          const float rc = 1.0f / sc;
+          if (slot < 0) continue;
+          uint8_t* qrow = p.cq + (int64_t)slot * p.inter;
+#pragma unroll
+          for (int jq = 0; jq < NB / 2 * 4; ++jq) {
+            const int jj = jq / 4, q = jq % 4;
+            const int gcol = nt * (BN / 2) + wn * (WTN / 2) + jj * 32 + 8 * q + 4 * lh;
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float x = av[i][jj][4 * q + e];
+              const float y0 = x * rc;
+              y[e] = clamp_fp8(__builtin_fmaf(__builtin_fmaf(-y0, sc, x), rc, y0));
+            }
+            *(int*)(qrow + gcol) = cvt_fp8x4(y[0], y[1], y[2], y[3]);
           }
-          if (gcol + 3 < p.inter && (p.ldc & 3) == 0) {
-            *(uint2*)(crow + gcol) = make_uint2(packed[0], packed[1]);
-          } else {
-            for (int e = 0; e < 4 && gcol + e < p.inter; ++e)
-              crow[gcol + e] = (uint16_t)(packed[e >> 1] >> (16 * (e & 1)));
-          }
+          if (wn == 0 && lh == 0) p.cs[(int64_t)slot * (p.inter / 128) + nt] = sc;
         }
       } else {
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          const int slot = slot_of(t, buf, wm * WTM + i * 32 + l32);
+          if (slot < 0) continue;
+          uint16_t* crow = C + (int64_t)slot * p.ldc;
+#pragma unroll
+          for (int jq = 0; jq < NB / 2 * 4; ++jq) {
+            const int jj = jq / 4, q = jq % 4;
+            const int gcol = nt * (BN / 2) + wn * (WTN / 2) + jj * 32 + 8 * q + 4 * lh;
+            if (gcol >= p.inter) continue;
+            uint32_t packed[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              packed[h] = (uint32_t)f32_to_bf16_bits(av[i][jj][4 * q + 2 * h]) |
+                          ((uint32_t)f32_to_bf16_bits(av[i][jj][4 * q + 2 * h + 1]) << 16);
+            if (gcol + 3 < p.inter && (p.ldc & 3) == 0) {
+              *(uint2*)(crow + gcol) = make_uint2(packed[0], packed[1]);
+            } else {
+              for (int e = 0; e < 4 && gcol + e < p.inter; ++e)
+                crow[gcol + e] = (uint16_t)(packed[e >> 1] >> (16 * (e & 1)));
+            }
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const int slot = slot_of(t, buf, wm * WTM + i * 32 + l32);
+        if (slot < 0) continue;
+        uint16_t* crow = C + (int64_t)slot * p.ldc;
         const float* meta = (const float*)(sMeta + buf * kBigMetaInts);
         const int row = wm * WTM + i * 32 + l32;
         float rs = 1.f;
@@ -439,6 +504,10 @@ static int run_big(const GemmArgs& a, hipStream_t stream) {
 }
 
 int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t stream) {
+  if (a.cq && (epi != EPI_ACT || a.inter % 128 != 0 || !a.cs)) {
+    set_last_error("gemm_fp8_big: fused quantisation needs the activation epilogue and inter %% 128 == 0");
+    return kInvalidArgument;
+  }
   if (a.K <= 0 || a.K % 128 != 0 || (epi == EPI_ACT && (a.N != 2 * a.inter))) {
     set_last_error("gemm_fp8_big: K must be a positive multiple of 128 (and N == 2 * inter)");
     return kInvalidArgument;

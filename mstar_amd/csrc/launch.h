@@ -30,8 +30,13 @@ size_t align_scratch_bytes(int64_t numel, int E);
 int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, int renorm,
                  float* w, int32_t* ids32, int64_t* ids64, int bm, int32_t* sorted_ids,
                  int32_t* expert_ids, int32_t* ntpp, int64_t max_padded, int32_t* expert_off,
-                 int32_t* expert_cnt, void* scratch, size_t scratch_bytes, hipStream_t stream);
+                 int32_t* expert_cnt, void* scratch, size_t scratch_bytes, hipStream_t stream,
+                 const void* hidden = nullptr, int64_t H = 0, uint8_t* hq = nullptr,
+                 float* hs = nullptr);
 size_t route_scratch_bytes(int64_t M, int k, int E);
+// Whether launch_route takes the multi-workgroup path for M tokens (the one
+// that can quantise the hidden rows on the way).
+bool route_is_grid(int64_t M, int k);
 
 // quant.hip
 // widen: q receives the e4m3fn values widened to bf16 (2 bytes per element).
@@ -83,6 +88,12 @@ struct GemmArgs {
   int activation;     // 0 silu, 1 gelu
   int num_experts;
   int m_blocks;       // grouped: number of m-blocks (expert_ids length)
+  // EPI_ACT of the 256-row FP8 kernel: when set, the activation output is
+  // quantised per token and group of 128 columns in the epilogue (e4m3fn
+  // codes cq [rows, inter], fp32 scales cs [rows, inter/128]) instead of
+  // being stored to C.
+  uint8_t* cq;
+  float* cs;
   // Streaming FP8 kernels only: when set, the per-expert slot lists are
   // built from these [M] router ids (int32 or int64, ids_dtype) instead of
   // sorted_ids / expert_off / expert_cnt.

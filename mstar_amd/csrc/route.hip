@@ -183,7 +183,7 @@ constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kAlignBatch = 16;          // ids held per lane per batch
 constexpr int kRouteSmallSlots = 4096;   // numel served by one workgroup
-constexpr int kRouteTokensPerBlock = 128;
+constexpr int kRouteTokensPerBlock = 32;  // 256 workgroups at 8192 tokens
 
 // Expert of slot i, or E for "skip" (out of range / beyond the end).
 template <typename IT>
@@ -294,10 +294,12 @@ __device__ __forceinline__ void write_meta(const int* off, const int* tot, int E
   if (expert_cnt)
     for (int e = tid; e < E; e += kAlignThreads) expert_cnt[e] = tot[e];
   const int64_t max_blocks = (max_padded + bm - 1) / bm;
-  for (int e = tid; e < E; e += kAlignThreads) {
+  for (int e = tid; e < E; e += kAlignThreads)
     for (int i = off[e]; i < off[e + 1]; i += bm) expert_ids[i / bm] = e;
-    for (int i = off[e] + tot[e]; i < off[e + 1]; ++i) sorted_ids[i] = (int32_t)numel;
-  }
+  // Padding slots of each expert: a group of G threads per expert.
+  const int G = E >= kAlignThreads ? 1 : kAlignThreads / E;
+  for (int e = tid / G; e < E; e += kAlignThreads / G)
+    for (int i = off[e] + tot[e] + tid % G; i < off[e + 1]; i += G) sorted_ids[i] = (int32_t)numel;
   for (int64_t i = total_padded / bm + tid; i < max_blocks; i += kAlignThreads) expert_ids[i] = 0;
   for (int64_t i = total_padded + tid; i < max_padded; i += kAlignThreads)
     sorted_ids[i] = (int32_t)numel;
@@ -391,11 +393,15 @@ __global__ __launch_bounds__(kAlignThreads) void route_small_kernel(
 
 // ---- grid-wide path --------------------------------------------------------
 // Pass 1 (top-k variant): top-k of kRouteTokensPerBlock tokens per workgroup
-// and the workgroup's expert histogram hist[b][E].
+// and the workgroup's expert histogram hist[b][E].  With `hidden` (bf16
+// [M, H], H % 128 == 0) the workgroup also quantises its tokens' hidden rows
+// per group of 128 into e4m3fn codes hq [M, H] and scales hs [M, H/128].
 template <typename LT, int EPL>
 __global__ __launch_bounds__(kAlignThreads) void topk_hist_kernel(
     const LT* __restrict__ logits, int64_t M, int E, int k, int renorm, float* __restrict__ w_out,
-    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, int32_t* __restrict__ hist) {
+    int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, int32_t* __restrict__ hist,
+    const uint16_t* __restrict__ hidden, int64_t H, uint8_t* __restrict__ hq,
+    float* __restrict__ hs) {
   extern __shared__ int smem[];
   int* h = smem;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -410,6 +416,31 @@ __global__ __launch_bounds__(kAlignThreads) void topk_hist_kernel(
                          if (ids64) ids64[t * k + r] = id;
                          atomicAdd(&h[id], 1);
                        });
+  if (hidden) {
+    // 8-element chunks of the block's rows; 16 consecutive chunks (16
+    // lanes) form one group of 128.
+    constexpr int kQB = 4;
+    const int64_t chunks = (t1 - t0) * (H / 8);
+    const uint16_t* src = hidden + t0 * H;
+    for (int64_t c0 = threadIdx.x; c0 < chunks; c0 += kQB * kAlignThreads) {
+      v4i raw[kQB];
+#pragma unroll
+      for (int b = 0; b < kQB; ++b) {
+        const int64_t c = c0 + (int64_t)b * kAlignThreads;
+        raw[b] = c < chunks ? *(const v4i*)(src + c * 8) : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int b = 0; b < kQB; ++b) {
+        const int64_t c = c0 + (int64_t)b * kAlignThreads;
+        float sc;
+        const int2 codes = quant_group8<kBF16>(raw[b], sc);
+        if (c < chunks) {
+          *(int2*)(hq + t0 * H + c * 8) = codes;
+          if ((lane & 15) == 0) hs[t0 * (H / 128) + c / 16] = sc;
+        }
+      }
+    }
+  }
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += kAlignThreads) hist[(int64_t)blockIdx.x * E + e] = h[e];
 }
@@ -449,17 +480,37 @@ __global__ __launch_bounds__(kAlignThreads) void scatter_kernel(
   int* base = tot + E;                // [E]
   int* wsum = base + E;               // [16]
   const int b = blockIdx.x;
-  for (int e = threadIdx.x; e < E; e += kAlignThreads) {
-    int pre = 0, all = 0;
-    for (int bb = 0; bb < nblocks; ++bb) {
-      const int c = hist[(int64_t)bb * E + e];
-      pre += bb < b ? c : 0;
-      all += c;
+  {
+    // Column sums of hist: `segs` threads per expert each add every
+    // segs-th row (loads unrolled so they overlap), then one thread per
+    // expert adds the partial sums.  wcnt holds the partials.
+    const int segs = E * 8 <= kAlignThreads ? 8 : kAlignThreads / E;
+    int* pall = wcnt;
+    int* ppre = wcnt + segs * E;
+    if (threadIdx.x < segs * E) {
+      const int e = threadIdx.x % E, sg = threadIdx.x / E;
+      int pre = 0, all = 0;
+#pragma unroll 8
+      for (int bb = sg; bb < nblocks; bb += segs) {
+        const int c = hist[(int64_t)bb * E + e];
+        pre += bb < b ? c : 0;
+        all += c;
+      }
+      pall[sg * E + e] = all;
+      ppre[sg * E + e] = pre;
     }
-    tot[e] = all;
-    base[e] = pre;
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += kAlignThreads) {
+      int pre = 0, all = 0;
+      for (int sg = 0; sg < segs; ++sg) {
+        all += pall[sg * E + e];
+        pre += ppre[sg * E + e];
+      }
+      tot[e] = all;
+      base[e] = pre;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   expert_scan(tot, E, bm, off, wsum);
   if (b == 0)
     write_meta(off, tot, E, bm, numel, max_padded, sorted_ids, expert_ids, ntpp, expert_off,
@@ -569,6 +620,8 @@ size_t align_scratch_bytes(int64_t numel, int E) {
   return (size_t)(blocks > 0 ? blocks : 1) * E * sizeof(int32_t);
 }
 
+bool route_is_grid(int64_t M, int k) { return M * k > kRouteSmallSlots; }
+
 size_t route_scratch_bytes(int64_t M, int k, int E) {
   const int64_t blocks = (M + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock;
   return (size_t)(blocks > 0 ? blocks : 1) * E * sizeof(int32_t) + (size_t)M * k * sizeof(int32_t);
@@ -631,7 +684,8 @@ static int route_impl(const void* logits, int64_t M, int E, int k, int renorm, f
                       int32_t* ids32, int64_t* ids64, int bm, int32_t* sorted_ids,
                       int32_t* expert_ids, int32_t* ntpp, int64_t max_padded, int32_t* expert_off,
                       int32_t* expert_cnt, void* scratch, size_t scratch_bytes,
-                      hipStream_t stream) {
+                      hipStream_t stream, const uint16_t* hidden, int64_t H, uint8_t* hq,
+                      float* hs) {
   const int64_t numel = M * k;
   int st;
   if (numel <= kRouteSmallSlots) {
@@ -652,7 +706,7 @@ static int route_impl(const void* logits, int64_t M, int E, int k, int renorm, f
   int32_t* hist = (int32_t*)scratch;
   int32_t* tmp_ids = ids32 ? ids32 : hist + (size_t)nblocks * E;
   topk_hist_kernel<LT, EPL><<<nblocks, kAlignThreads, E * sizeof(int), stream>>>(
-      (const LT*)logits, M, E, k, renorm, w, tmp_ids, ids64, hist);
+      (const LT*)logits, M, E, k, renorm, w, tmp_ids, ids64, hist, hidden, H, hq, hs);
   const size_t sshm = scatter_lds(E);
   static size_t done = 0;
   if ((st = opt_in_lds(scatter_kernel<GlobalIds<int32_t>>, sshm, done)) != kOk) return st;
@@ -665,7 +719,8 @@ static int route_impl(const void* logits, int64_t M, int E, int k, int renorm, f
 int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, int renorm,
                  float* w, int32_t* ids32, int64_t* ids64, int bm, int32_t* sorted_ids,
                  int32_t* expert_ids, int32_t* ntpp, int64_t max_padded, int32_t* expert_off,
-                 int32_t* expert_cnt, void* scratch, size_t scratch_bytes, hipStream_t stream) {
+                 int32_t* expert_cnt, void* scratch, size_t scratch_bytes, hipStream_t stream,
+                 const void* hidden, int64_t H, uint8_t* hq, float* hs) {
   if (M < 0 || k <= 0 || k > 64 || k > E || !w || (M > 0 && !logits)) {
     set_last_error("moe_route: invalid arguments (M=%lld E=%d k=%d)", (long long)M, E, k);
     return kInvalidArgument;
@@ -676,15 +731,22 @@ int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, 
     set_last_error("moe_route: logits must be float32 or bfloat16");
     return kUnsupported;
   }
+  if (hidden && (!route_is_grid(M, k) || H <= 0 || H % 128 != 0 || !hq || !hs)) {
+    set_last_error("moe_route: hidden-row quantisation needs the multi-workgroup path and "
+                   "H %% 128 == 0 (M=%lld H=%lld)", (long long)M, (long long)H);
+    return kInvalidArgument;
+  }
+  const uint16_t* hid = (const uint16_t*)hidden;
   const int epl = (E + 63) / 64;
 #define MSTAR_ROUTE(N)                                                                          \
   return logits_dtype == kF32                                                                   \
              ? route_impl<float, N>(logits, M, E, k, renorm, w, ids32, ids64, bm, sorted_ids,   \
                                     expert_ids, ntpp, max_padded, expert_off, expert_cnt,       \
-                                    scratch, scratch_bytes, stream)                             \
+                                    scratch, scratch_bytes, stream, hid, H, hq, hs)             \
              : route_impl<uint16_t, N>(logits, M, E, k, renorm, w, ids32, ids64, bm,            \
                                        sorted_ids, expert_ids, ntpp, max_padded, expert_off,    \
-                                       expert_cnt, scratch, scratch_bytes, stream);
+                                       expert_cnt, scratch, scratch_bytes, stream, hid, H, hq,  \
+                                       hs);
   if (epl <= 1) { MSTAR_ROUTE(1) }
   if (epl <= 2) { MSTAR_ROUTE(2) }
   if (epl <= 4) { MSTAR_ROUTE(4) }

@@ -293,10 +293,13 @@ def test_layer_under_hip_graph_replays():
 
 
 @pytest.mark.parametrize("M,bias,quant", [(32, False, "fp8_w8a8"), (8, False, "fp8_w8a8"),
-                                          (512, True, "fp8_w8a8"), (16, False, None),
+                                          (512, True, "fp8_w8a8"), (1024, True, "fp8_w8a8"),
+                                          (4096, True, "fp8_w8a8"), (16, False, None),
                                           (32, False, "w4a16")])
 def test_moe_layer_from_logits(M, bias, quant):
-    """Routing from logits + experts in one library call (mstar_moe_layer)."""
+    """Routing from logits + experts in one library call (mstar_moe_layer).
+    From 4096 slots up the multi-workgroup routing also quantises the hidden
+    rows; at M=4096 the 256-row FP8 tile kernel runs."""
     from mstar_amd import _lib, ops, quant as Q
     H, E, I, k = 2048, 128, 768, 8
     x = _hidden(M, H, seed=M + 21)
@@ -331,7 +334,7 @@ def test_moe_layer_from_logits(M, bias, quant):
 
 @pytest.mark.parametrize("M,E,k,H,I,bias", [(1024, 16, 4, 512, 256, False), (2048, 32, 8, 1024, 384, True)])
 def test_fused_experts_fp8_big_tile_path(M, E, k, H, I, bias):
-    """>= 256 slots per expert on average selects the 256 x 128 FP8 tile kernel."""
+    """>= 256 slots per expert on average selects the 256 x 256 FP8 tile kernel."""
     from mstar_amd.fused_moe import fused_experts
     q1, s1, q2, s2 = _fp8_weights(H, E, I, seed=9)
     x = _hidden(M, H, seed=9)
