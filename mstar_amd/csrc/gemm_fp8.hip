@@ -267,6 +267,18 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
 #pragma unroll
   for (int n = 0; n < kParts; ++n) issue_part(n, ik, ist);
 
+  // Output buffers (sizes below 4 GiB: checked on the host).
+  const auto rs_c = make_rsrc(p.C, (uint32_t)((int64_t)p.M * p.ldc * 2));
+  const auto rs_cq = make_rsrc(p.cq, (uint32_t)((int64_t)p.M * p.inter));
+  const auto rs_cs = make_rsrc(p.cs, (uint32_t)((int64_t)p.M * (p.inter / 128) * 4));
+  // Stores each wave issues in a tile's epilogue (0: a path with a variable
+  // count, waited for in full).
+  int epi_stores;
+  if constexpr (EPI == EPI_ACT)
+    epi_stores = p.cq ? BM / 8 / 8 + MB : ((p.ldc & 7) == 0 && (p.inter & 7) == 0) ? BM / 8 / 4 : 0;
+  else
+    epi_stores = ((p.ldc & 7) == 0 && (p.N & 7) == 0) ? MB * 8 : 0;
+
   for (int j = 0; tile_of(j) < total; ++j) {
     const int t = tile_of(j);
     const int mb = t / n_tiles, nt = t - mb * n_tiles;
@@ -280,8 +292,13 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
 
     for (int kb = 0; kb < KB; ++kb) {
       const int q = j * KB + kb;  // global step of this computation
-      // Step q is the only one in flight: wait for it.
-      wait_vmcnt<0>();
+      // Step q is the only DMA in flight: wait for it.  At a tile's first
+      // step the previous epilogue's stores, issued after it, may still be
+      // draining: they are left in flight.
+      if (kb == 0 && j > 0 && epi_stores == MB * 8) wait_vmcnt<MB * 8>();
+      else if (kb == 0 && j > 0 && epi_stores == BM / 8 / 4) wait_vmcnt<BM / 8 / 4>();
+      else if (kb == 0 && j > 0 && epi_stores == BM / 8 / 8 + MB) wait_vmcnt<BM / 8 / 8 + MB>();
+      else wait_vmcnt<0>();
       // Step q has landed for every wave, and every wave is past step q-1,
       // whose stage the next issue overwrites.
       lds_barrier();
@@ -346,10 +363,25 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
       }
     }
 
-    // ---- epilogue, straight from registers (the ring keeps loading the
-    // next tile).  Lane (l32, lh), register e of tile (i, jj): token row
-    // wm*WTM + i*32 + l32, weight column wn*WTN + jj*32 + 8*(e/4) + 4*lh + (e%4).
+    // ---- epilogue (the ring keeps loading the next tile meanwhile).  Lane
+    // (l32, lh), register e of tile (i, jj): token row wm*WTM + i*32 + l32,
+    // weight column wn*WTN + jj*32 + 8*(e/4) + 4*lh + (e%4).  Results are
+    // staged in the ring stage of the tile's last step (free once every wave
+    // is past its MFMAs) and leave as whole contiguous row segments, 16
+    // bytes per lane: stored straight from the MFMA layout, every store
+    // instruction would touch 32 rows.  Staged rows are split in 16-byte
+    // units, unit u of row r kept at position u ^ (r % units-per-row).
     uint16_t* C = (uint16_t*)p.C;
+    uint8_t* stg = smem + (size_t)((j * KB + KB - 1) % kBigStages) * kBigStageBytes;
+    // Lane-derived addresses are computed here, per tile: hoisted out of
+    // the tile loop they outlive the accumulators' register budget and are
+    // spilled, and every reload would wait for the DMA and stores in flight.
+    int lane_e;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(lane_e) : "v"(lane));
+    const int l32 = lane_e & 31, lh = lane_e >> 5;
+    // The staged paths store through buffer resources: a lane with nothing
+    // to write stores out of range (dropped), so every wave issues a fixed
+    // number of stores per tile -- the next tile's first wait counts them.
     if constexpr (EPI == EPI_ACT) {
       // a = bf16(bf16(act(bf16(gate))) * bf16(up)): the values the
       // reference's act_and_mul writes (kernels.py:279-298).
@@ -374,7 +406,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
         // tile's columns: amax over the lane pair (lh) and the wave columns
         // (through LDS), scale = max(amax, eps) / 448, codes = a / scale
         // rounded to e4m3fn.  The quotient is a * (1/scale) corrected by one
-        // FMA residual step, which rounds like the IEEE division.
+        // FMA residual step, which rounds like the IEEE division.  Staged
+        // as 256 rows of 128 code bytes (8 units).
         float* sAmax = (float*)(smem + kBigRedOff);  // [WN][BM]
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
@@ -386,22 +419,19 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
           m = fmaxf(m, __shfl_xor(m, 32));
           if (lh == 0) sAmax[wn * BM + wm * WTM + i * 32 + l32] = m;
         }
-        lds_sync();
+        lds_sync();  // also: every wave is past its MFMAs, the stage is free
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
           const int row = wm * WTM + i * 32 + l32;
-          const int slot = slot_of(t, buf, row);
           float m = sAmax[row];
 #pragma unroll
           for (int ww = 1; ww < WN; ++ww) m = fmaxf(m, sAmax[ww * BM + row]);
           const float sc = fmaxf(m, kQuantEps) / kFp8Max;
           const float rc = 1.0f / sc;
-          if (slot < 0) continue;
-          uint8_t* qrow = p.cq + (int64_t)slot * p.inter;
 #pragma unroll
           for (int jq = 0; jq < NB / 2 * 4; ++jq) {
             const int jj = jq / 4, q = jq % 4;
-            const int gcol = nt * (BN / 2) + wn * (WTN / 2) + jj * 32 + 8 * q + 4 * lh;
+            const int cb = wn * (WTN / 2) + jj * 32 + 8 * q + 4 * lh;  // code byte in the row
             float y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -409,9 +439,51 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
               const float y0 = x * rc;
               y[e] = clamp_fp8(__builtin_fmaf(__builtin_fmaf(-y0, sc, x), rc, y0));
             }
-            *(int*)(qrow + gcol) = cvt_fp8x4(y[0], y[1], y[2], y[3]);
+            *(int*)(stg + row * 128 + (((cb >> 4) ^ (row & 7)) << 4) + (cb & 15)) =
+                cvt_fp8x4(y[0], y[1], y[2], y[3]);
           }
-          if (wn == 0 && lh == 0) p.cs[(int64_t)slot * (p.inter / 128) + nt] = sc;
+          {  // one lane per token writes the scale; the others' stores fall outside the buffer
+            const int slot = slot_of(t, buf, row);
+            const uint32_t off = slot >= 0 && wn == 0 && lh == 0
+                                     ? (uint32_t)(((int64_t)slot * (p.inter / 128) + nt) * 4) : kOffNone;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, sc), rs_cs, off, 0, 0);
+          }
+        }
+        lds_sync();
+#pragma unroll
+        for (int pass = 0; pass < BM / 8 / 8; ++pass) {  // 8 rows per wave instruction
+          const int row = wave * (BM / 8) + pass * 8 + (lane_e >> 3), u = lane_e & 7;
+          const v4i val = *(const v4i*)(stg + row * 128 + ((u ^ (row & 7)) << 4));
+          const int slot = slot_of(t, buf, row);
+          const uint32_t off = slot >= 0 ? (uint32_t)((int64_t)slot * p.inter + nt * (BN / 2) + u * 16) : kOffNone;
+          __builtin_amdgcn_raw_buffer_store_b128(val, rs_cq, off, 0, 0);
+        }
+      } else if ((p.ldc & 7) == 0 && (p.inter & 7) == 0) {
+        // 256 rows of 128 bf16 (16 units).
+        lds_barrier();  // every wave is past its MFMAs: the stage is free
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          const int row = wm * WTM + i * 32 + l32;
+#pragma unroll
+          for (int jq = 0; jq < NB / 2 * 4; ++jq) {
+            const int jj = jq / 4, q = jq % 4;
+            const int u = wn * (WTN / 16) + jj * 4 + q;
+            const uint32_t lo = (uint32_t)f32_to_bf16_bits(av[i][jj][4 * q]) |
+                                ((uint32_t)f32_to_bf16_bits(av[i][jj][4 * q + 1]) << 16);
+            const uint32_t hi = (uint32_t)f32_to_bf16_bits(av[i][jj][4 * q + 2]) |
+                                ((uint32_t)f32_to_bf16_bits(av[i][jj][4 * q + 3]) << 16);
+            *(uint2*)(stg + row * 256 + ((u ^ (row & 15)) << 4) + lh * 8) = make_uint2(lo, hi);
+          }
+        }
+        lds_sync();
+#pragma unroll
+        for (int pass = 0; pass < BM / 8 / 4; ++pass) {  // 4 rows per wave instruction
+          const int row = wave * (BM / 8) + pass * 4 + (lane_e >> 4), u = lane_e & 15;
+          const v4i val = *(const v4i*)(stg + row * 256 + ((u ^ (row & 15)) << 4));
+          const int slot = slot_of(t, buf, row);
+          const int gcol = nt * (BN / 2) + u * 8;
+          const uint32_t off = slot >= 0 && gcol < p.inter ? (uint32_t)(((int64_t)slot * p.ldc + gcol) * 2) : kOffNone;
+          __builtin_amdgcn_raw_buffer_store_b128(val, rs_c, off, 0, 0);
         }
       } else {
 #pragma unroll
@@ -423,53 +495,72 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
           for (int jq = 0; jq < NB / 2 * 4; ++jq) {
             const int jj = jq / 4, q = jq % 4;
             const int gcol = nt * (BN / 2) + wn * (WTN / 2) + jj * 32 + 8 * q + 4 * lh;
-            if (gcol >= p.inter) continue;
-            uint32_t packed[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-              packed[h] = (uint32_t)f32_to_bf16_bits(av[i][jj][4 * q + 2 * h]) |
-                          ((uint32_t)f32_to_bf16_bits(av[i][jj][4 * q + 2 * h + 1]) << 16);
-            if (gcol + 3 < p.inter && (p.ldc & 3) == 0) {
-              *(uint2*)(crow + gcol) = make_uint2(packed[0], packed[1]);
-            } else {
-              for (int e = 0; e < 4 && gcol + e < p.inter; ++e)
-                crow[gcol + e] = (uint16_t)(packed[e >> 1] >> (16 * (e & 1)));
-            }
+            for (int e = 0; e < 4 && gcol + e < p.inter; ++e)
+              crow[gcol + e] = f32_to_bf16_bits(av[i][jj][4 * q + e]);
           }
         }
       }
     } else {
+      // Row factor (routed weight or dense A-row scale) and, dense, the
+      // column scales.
+      const float* meta = (const float*)(sMeta + buf * kBigMetaInts);
+      auto row_factor = [&](int row, int slot) -> float {
+        if constexpr (EPI == EPI_DENSE) return meta[BM + row];
+        if (!p.mul_routed) return 1.f;
+        return p.topk_w_dtype == kF32 ? meta[BM + row] : load_weight_any(p.topk_w, p.topk_w_dtype, slot);
+      };
+      auto scaled4 = [&](int i, int jj, int q, float rs, int lcol, uint32_t& lo, uint32_t& hi) {
+        float v[4];
 #pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        const int slot = slot_of(t, buf, wm * WTM + i * 32 + l32);
-        if (slot < 0) continue;
-        uint16_t* crow = C + (int64_t)slot * p.ldc;
-        const float* meta = (const float*)(sMeta + buf * kBigMetaInts);
-        const int row = wm * WTM + i * 32 + l32;
-        float rs = 1.f;
-        if constexpr (EPI == EPI_DENSE) rs = meta[BM + row];
-        else if (p.mul_routed)
-          rs = p.topk_w_dtype == kF32 ? meta[BM + row] : load_weight_any(p.topk_w, p.topk_w_dtype, slot);
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[i][jj][4 * q + e] * rs;
+          if constexpr (EPI == EPI_DENSE) v[e] *= meta[2 * BM + lcol + e];
+        }
+        lo = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+        hi = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+      };
+      if ((p.ldc & 7) == 0 && (p.N & 7) == 0) {
+        // Two halves (row tiles i = 0, 1) of 128 rows x 256 bf16 (32 units).
+        lds_barrier();  // every wave is past its MFMAs: the stage is free
 #pragma unroll
-        for (int jj = 0; jj < NB; ++jj) {
+        for (int i = 0; i < MB; ++i) {
+          const int row = wm * WTM + i * 32 + l32, lr = wm * 32 + l32;
+          const float rs = row_factor(row, slot_of(t, buf, row));
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int col = nt * BN + wn * WTN + jj * 32 + 8 * q + 4 * lh;
-            if (col >= p.N) continue;
-            float v[4];
+          for (int jq = 0; jq < NB * 4; ++jq) {
+            const int jj = jq / 4, q = jq % 4;
+            const int lcol = wn * WTN + jj * 32 + 8 * q + 4 * lh;
+            uint32_t lo, hi;
+            scaled4(i, jj, q, rs, lcol, lo, hi);
+            *(uint2*)(stg + lr * 512 + (((lcol >> 3) ^ (lr & 31)) << 4) + lh * 8) = make_uint2(lo, hi);
+          }
+          lds_sync();
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v[e] = acc[i][jj][4 * q + e] * rs;
-              if constexpr (EPI == EPI_DENSE) v[e] *= meta[2 * BM + (col + e - nt * BN)];
-            }
-            if (col + 3 < p.N && (p.ldc & 3) == 0) {
-              const uint32_t lo = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
-              const uint32_t hi = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
-              *(uint2*)(crow + col) = make_uint2(lo, hi);
-            } else {
-              for (int e = 0; e < 4; ++e)
-                if (col + e < p.N) crow[col + e] = f32_to_bf16_bits(v[e]);
-            }
+          for (int pass = 0; pass < 8; ++pass) {  // 2 rows per wave instruction
+            const int lr2 = wave * 16 + pass * 2 + (lane_e >> 5), u = lane_e & 31;
+            const v4i val = *(const v4i*)(stg + lr2 * 512 + ((u ^ (lr2 & 31)) << 4));
+            const int slot = slot_of(t, buf, (lr2 >> 5) * WTM + i * 32 + (lr2 & 31));
+            const int col = nt * BN + u * 8;
+            const uint32_t off = slot >= 0 && col < p.N ? (uint32_t)(((int64_t)slot * p.ldc + col) * 2) : kOffNone;
+            __builtin_amdgcn_raw_buffer_store_b128(val, rs_c, off, 0, 0);
+          }
+          if (i + 1 < MB) lds_barrier();  // half i is read before half i + 1 lands
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          const int row = wm * WTM + i * 32 + l32;
+          const int slot = slot_of(t, buf, row);
+          if (slot < 0) continue;
+          uint16_t* crow = C + (int64_t)slot * p.ldc;
+          const float rs = row_factor(row, slot);
+#pragma unroll
+          for (int jq = 0; jq < NB * 4; ++jq) {
+            const int jj = jq / 4, q = jq % 4;
+            const int lcol = wn * WTN + jj * 32 + 8 * q + 4 * lh, col = nt * BN + lcol;
+            uint32_t w2[2];
+            scaled4(i, jj, q, rs, lcol, w2[0], w2[1]);
+            for (int e = 0; e < 4 && col + e < p.N; ++e) crow[col + e] = (uint16_t)(w2[e >> 1] >> (16 * (e & 1)));
           }
         }
       }
@@ -504,6 +595,10 @@ static int run_big(const GemmArgs& a, hipStream_t stream) {
 }
 
 int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t stream) {
+  if (a.M * a.ldc * 2 >= (int64_t)kOffNone || a.M * a.inter >= (int64_t)kOffNone) {
+    set_last_error("gemm_fp8_big: output larger than 4 GiB");
+    return kUnsupported;
+  }
   if (a.cq && (epi != EPI_ACT || a.inter % 128 != 0 || !a.cs)) {
     set_last_error("gemm_fp8_big: fused quantisation needs the activation epilogue and inter %% 128 == 0");
     return kInvalidArgument;
