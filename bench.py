@@ -47,10 +47,10 @@ COPY_BYTES = 512 << 20
 # from two rocprofv3 --pmc passes over `bench.py --kernel-only` (FETCH_SIZE,
 # then WRITE_SIZE; KiB per dispatch, mean of 24 dispatches).  Each counter
 # is scaled by what it reads for torch's neg kernel over COPY_BYTES in the
-# same run: FETCH_SIZE reports 262,153.5 KiB for the 524,288 KiB read
+# same run: FETCH_SIZE reports 262,150.6 KiB for the 524,288 KiB read
 # (x2.0), WRITE_SIZE 524,288 KiB for the 524,288 KiB written (x1.0).
-GATE_UP_FETCH_KIB, FETCH_FACTOR = 179044.1, 2.0
-GATE_UP_WRITE_KIB, WRITE_FACTOR = 594.0, 1.0
+GATE_UP_FETCH_KIB, FETCH_FACTOR = 177354.4, 2.0
+GATE_UP_WRITE_KIB, WRITE_FACTOR = 386.4, 1.0
 
 
 def parse():
