@@ -219,16 +219,22 @@ __device__ __forceinline__ int2 quant_group8(v4i raw, float& scale) {
                              clamp_fp8(f[7] / sc)));
 }
 
-// Inclusive prefix sum across the 64 lanes of a wave.
+// Inclusive prefix sum across the 64 lanes of a wave, by DPP: shifts by
+// 1, 2, 4 and 8 lanes within each row of 16, then the last lane of each row
+// broadcast into the rows after it (row_bcast:15 into rows 1 and 3,
+// row_bcast:31 into rows 2 and 3).  Lanes without a source add 0.
 __device__ inline int wave_incl_scan(int v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int t = __shfl_up(v, o, 64);
-    if (l >= o) v += t;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return v;
 }
+
+// Lane 63's value, wave-uniform (a scalar read, no LDS round trip).
+__device__ inline int wave_last(int v) { return __builtin_amdgcn_readlane(v, 63); }
 
 // ---------------------------------------------------------------- MFMA
 // 16x16x128 FP8 (e4m3fn x e4m3fn), fp32 accumulate.  Operand layout (both A

@@ -13,113 +13,10 @@
 //    with a ballot-based match (no atomics), so the scatter is stable.
 #include "common.h"
 #include "launch.h"
+#include "topk.h"
 
 namespace mstar {
 
-template <typename LT>
-__device__ inline float load_logit(const LT* p, int64_t i);
-template <>
-__device__ inline float load_logit<float>(const float* p, int64_t i) { return p[i]; }
-template <>
-__device__ inline float load_logit<uint16_t>(const uint16_t* p, int64_t i) {
-  return bf16_bits_to_f32(p[i]);
-}
-
-// Order-preserving map fp32 -> uint32 (larger float, larger key).
-__device__ __forceinline__ uint32_t float_key(float v) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, v);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Inverse of float_key.
-__device__ __forceinline__ float key_float(uint32_t k) {
-  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
-// Softmax top-k of one token by one wave (EPL = experts per lane,
-// ceil(E / 64); expert e sits in lane e % 64, slot e / 64).
-//
-// Selection: k rounds of argmax over order-preserving integer keys of the
-// logits (softmax is monotonic, so ranking logits ranks probabilities).
-// Each round is a DPP max over the wave, then a ballot for the lowest
-// expert index holding that key (ties go to the lower index), which is
-// removed for the next round.  Ranks come out in order (value descending,
-// ties by index).  The softmax max and sum are DPP reductions too; nothing
-// goes through LDS.  emit(rank, expert, weight) runs on lane `rank` for
-// each of the k selections (k <= 64).
-template <int EPL, typename Emit>
-__device__ __forceinline__ void topk_wave(const float (&v)[EPL], int E, int k, int renorm, int lane,
-                                          const Emit& emit) {
-  uint32_t key[EPL];
-  float mxl = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const bool valid = j * 64 + lane < E;
-    key[j] = valid ? float_key(v[j]) : 0u;  // 0 is below every valid key
-    mxl = fmaxf(mxl, valid ? v[j] : -INFINITY);
-  }
-  const float mx = wave_fmax_dpp(mxl);
-  float sl = 0.f;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) sl += j * 64 + lane < E ? __expf(v[j] - mx) : 0.f;
-  const float s = wave_fsum_dpp(sl);
-
-  float my_p = 0.f, psum = 0.f;
-  int my_id = 0;
-  for (int r = 0; r < k; ++r) {
-    uint32_t lm = key[0];
-#pragma unroll
-    for (int j = 1; j < EPL; ++j) lm = max(lm, key[j]);
-    const uint32_t m = wave_umax_dpp(lm);
-    int sel = -1;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const uint64_t b = __ballot(key[j] == m);
-      if (sel < 0 && b) sel = j * 64 + __builtin_ctzll(b);
-    }
-#pragma unroll
-    for (int j = 0; j < EPL; ++j)
-      if (sel == j * 64 + lane) key[j] = 0u;
-    const float p = __expf(key_float(m) - mx) / s;
-    psum += p;
-    if (lane == r) {
-      my_p = p;
-      my_id = sel;
-    }
-  }
-  if (lane < k) emit(lane, my_id, renorm ? my_p / psum : my_p);
-}
-
-// Top-k of tokens t0, t0 + stride, ... (< t1) by one wave, a batch at a
-// time: the logit rows of a batch are loaded together, so the wave waits
-// for memory once per batch instead of once per token (batch size shrinks
-// with the experts per lane to stay within 128 VGPRs).
-// emit(token, rank, expert, weight).
-template <typename LT, int EPL, typename Emit>
-__device__ __forceinline__ void topk_tokens(const LT* __restrict__ logits, int64_t t0, int64_t t1,
-                                            int64_t stride, int E, int k, int renorm, int lane,
-                                            const Emit& emit) {
-  constexpr int kTopkBatch = EPL >= 8 ? 1 : (EPL >= 4 ? 2 : 4);
-  for (int64_t tb = t0; tb < t1; tb += kTopkBatch * stride) {
-    float v[kTopkBatch][EPL];
-#pragma unroll
-    for (int b = 0; b < kTopkBatch; ++b) {
-      const int64_t t = tb + b * stride;
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) {
-        const int e = j * 64 + lane;
-        v[b][j] = (t < t1 && e < E) ? load_logit<LT>(logits + t * E, e) : -INFINITY;
-      }
-    }
-#pragma unroll
-    for (int b = 0; b < kTopkBatch; ++b) {
-      const int64_t t = tb + b * stride;
-      if (t >= t1) break;
-      topk_wave<EPL>(v[b], E, k, renorm, lane,
-                     [&](int r, int id, float w) { emit(t, r, id, w); });
-    }
-  }
-}
 
 // One wave per token.  With `hidden`, a second wave per token quantises the
 // token's bf16 hidden row per group of 128 for the FP8 expert GEMMs that

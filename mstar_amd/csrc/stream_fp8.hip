@@ -104,7 +104,7 @@ __device__ __forceinline__ void build_expert_lists(const GemmArgs& p, int tid, i
         const int c = e < E ? sCnt[e] : 0;
         const int incl = wave_incl_scan(c);
         if (e < E) sOff[e] = run + incl - c;
-        run += __shfl(incl, 63, 64);
+        run += wave_last(incl);
       }
     }
     __syncthreads();
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   // Active experts: prefix popcounts of the mask words (lane i: word i).
   const uint32_t mword = lane < 32 ? sMask[lane] : 0u;
   const int wincl = wave_incl_scan(__builtin_popcount(mword));
-  const int n_act = __shfl(wincl, 63, 64);
+  const int n_act = wave_last(wincl);
   const int total = n_act * IPE;
   const int T = (total + gridDim.x - 1) / gridDim.x;
   const int i0 = blockIdx.x * T;
@@ -512,7 +512,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
       const int c = e < E ? sCnt[e] : 0;
       const int incl = wave_incl_scan(c);
       if (e < E) sOff[e] = run + incl - c;
-      run += __shfl(incl, 63, 64);
+      run += wave_last(incl);
     }
     int n = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
@@ -717,7 +717,9 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
         // Wait for this chunk's DMA, leaving the later ones in flight (two
         // fewer, for the epilogue store / routed-weight load that may sit
         // between them: over-waiting is safe).
-        if (ahead >= 3) wait_vmcnt<(2 * DPC - 2 > 0 ? 2 * DPC - 2 : 0)>();
+        static_assert(kCuRing >= 3 && kCuRing <= 4, "waits below cover rings of 3 or 4 slots");
+        if (kCuRing >= 4 && ahead >= 4) wait_vmcnt<(3 * DPC - 2 > 0 ? 3 * DPC - 2 : 0)>();
+        else if (ahead >= 3) wait_vmcnt<(2 * DPC - 2 > 0 ? 2 * DPC - 2 : 0)>();
         else if (ahead == 2) wait_vmcnt<(DPC - 2 > 0 ? DPC - 2 : 0)>();
         else wait_vmcnt<0>();
         const uint8_t* wslot = ring + cslot * SLOT;

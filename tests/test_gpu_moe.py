@@ -332,6 +332,26 @@ def test_moe_layer_from_logits(M, bias, quant):
     assert_moe_close(out, ref, what=f"moe_layer M={M} {quant}")
 
 
+@pytest.mark.parametrize("M,renorm,E,k", [(24, False, 128, 8), (32, True, 128, 8), (5, True, 128, 8),
+                                          (16, True, 64, 6), (8, False, 100, 8)])
+def test_moe_layer_decode_bf16_logits(M, renorm, E, k):
+    """Decode layers (routing launch + router-ids GEMMs): bf16 logits (with
+    exact ties), both renormalisation settings and expert counts that are not
+    a multiple of 16 give the oracle's routing and output."""
+    from mstar_amd import _lib, ops
+    H, I = 2048, 768
+    x = _hidden(M, H, seed=M + 31)
+    g = torch.Generator().manual_seed(M + 32)
+    logits = (torch.randn(M, E, generator=g) * 0.5).to(torch.bfloat16)
+    rw, rids = O.router_topk_softmax(logits.float(), k, renorm)
+    q1, s1, q2, s2 = _fp8_weights(H, E, I)
+    out, tw, ti = ops.moe_layer(x.to(DEV), logits.to(DEV), q1, q2, k, renorm, 0,
+                                _lib.QUANT_FP8_W8A8, s1, s2)
+    assert torch.equal(ti.cpu(), rids)
+    torch.testing.assert_close(tw.cpu(), rw, rtol=2e-6, atol=1e-9)
+    assert_moe_close(out, _fp8_ref(x, q1, s1, q2, s2, rw, rids), what=f"decode layer bf16 logits M={M} E={E}")
+
+
 @pytest.mark.parametrize("M,E,k,H,I,bias", [(1024, 16, 4, 512, 256, False), (2048, 32, 8, 1024, 384, True)])
 def test_fused_experts_fp8_big_tile_path(M, E, k, H, I, bias):
     """>= 256 slots per expert on average selects the 256 x 256 FP8 tile kernel."""
