@@ -65,6 +65,20 @@ int mstar_moe_topk_softmax(const void* logits, int logits_dtype, int64_t num_tok
                            int num_experts, int top_k, int renormalize, float* topk_weights,
                            int32_t* topk_ids_i32, int64_t* topk_ids_i64, void* stream);
 
+/* Fused router: TopKRouter.forward (mstar/model/components/moe.py:114-140)
+ * from the hidden states on, in one launch: logits = bf16(hidden . gate_weight^T)
+ * (bf16 [num_tokens, hidden_size] x bf16 [num_experts, hidden_size], fp32
+ * accumulation -- F.linear), fp32 softmax, top-k (ties to the lower expert
+ * index), renormalisation if asked.  topk_weights fp32 [num_tokens, top_k];
+ * topk_ids int32 and/or int64 (either may be NULL, not both); logits_out
+ * (optional, bf16 [num_tokens, num_experts]) receives the logits.
+ * act_dtype must be MSTAR_DTYPE_BF16; hidden_size % 32 == 0,
+ * num_experts <= 256, top_k <= 64. */
+int mstar_moe_router(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                     const void* gate_weight, int num_experts, int top_k, int renormalize,
+                     float* topk_weights, int32_t* topk_ids_i32, int64_t* topk_ids_i64,
+                     void* logits_out, void* stream);
+
 /* mstar_moe_topk_softmax plus the per-token-group-128 FP8 quantisation of
  * the same tokens' hidden rows, in one launch (one wave per token): hidden
  * [num_tokens, hidden_size] bf16 -> hidden_q [num_tokens, hidden_size]

@@ -37,6 +37,8 @@ SIGNATURES = {
     "mstar_moe_last_error": (ctypes.c_char_p, []),
     "mstar_moe_abi_version": (_c_int, []),
     "mstar_moe_topk_softmax": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
+    "mstar_moe_router": (
+        _c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp]),
     "mstar_moe_topk_softmax_quant": (
         _c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp,
                  _vp]),

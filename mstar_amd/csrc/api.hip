@@ -249,6 +249,18 @@ int mstar_moe_topk_softmax(const void* logits, int logits_dtype, int64_t num_tok
                              topk_weights, topk_ids_i32, topk_ids_i64, (hipStream_t)stream);
 }
 
+int mstar_moe_router(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                     const void* gate_weight, int num_experts, int top_k, int renormalize,
+                     float* topk_weights, int32_t* topk_ids_i32, int64_t* topk_ids_i64,
+                     void* logits_out, void* stream) {
+  if (act_dtype != kBF16) {
+    set_last_error("router: hidden states and gate weight must be bfloat16");
+    return kUnsupported;
+  }
+  return launch_router(hidden, num_tokens, hidden_size, gate_weight, num_experts, top_k, renormalize,
+                       topk_weights, topk_ids_i32, topk_ids_i64, logits_out, (hipStream_t)stream);
+}
+
 int mstar_moe_topk_softmax_quant(const void* logits, int logits_dtype, int64_t num_tokens,
                                  int num_experts, int top_k, int renormalize,
                                  float* topk_weights, int32_t* topk_ids_i32,

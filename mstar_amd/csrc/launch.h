@@ -12,6 +12,11 @@ namespace mstar {
 // With `hidden` (bf16 [M, H], H % 512 == 0) the launch also quantises the
 // hidden rows per group of 128: hq [M, H] holds the e4m3fn values widened to
 // bf16, hs [M, H/128] the scales.
+// Fused router (router.hip): bf16 hidden [M, H] x bf16 gate weight [E, H]
+// -> bf16 logits (optionally stored), softmax top-k, renormalisation.
+int launch_router(const void* hidden, int64_t M, int64_t H, const void* gate_weight, int E, int k,
+                  int renorm, float* w, int32_t* ids32, int64_t* ids64, void* logits_out,
+                  hipStream_t stream);
 int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, int k,
                         int renorm, float* w, int32_t* ids32, int64_t* ids64, hipStream_t stream,
                         const void* hidden = nullptr, int64_t H = 0, uint16_t* hq = nullptr,

@@ -1,8 +1,10 @@
 """MoE blocks and the router (drop-in for mstar/model/components/moe.py).
 
-* :class:`TopKRouter` -- ``F.linear`` gate projection, then the HIP
-  softmax-top-k kernel (moe.py:85-140); returns ``(weights fp32, ids int64,
-  None)`` like the reference's 3-tuple router contract.
+* :class:`TopKRouter` -- gate projection, softmax, top-k and renormalisation
+  (moe.py:85-140): one fused HIP launch for bf16 states and weights (the
+  reference's dtype), else ``F.linear`` then the HIP softmax-top-k kernel;
+  returns ``(weights fp32, ids int64, None)`` like the reference's 3-tuple
+  router contract.
 * :func:`dispatch` -- the fused path (moe.py:188-205 minus the naive
   fallback: these kernels are the only compute path; CPU tensors raise).
 * :class:`SparseMoeBlock` / :class:`SparseMoeBlockWithSharedExpert` --
@@ -32,6 +34,10 @@ class TopKRouter(nn.Module):
 
     def forward(self, hidden_states: torch.Tensor, router_states: torch.Tensor | None = None):
         hidden_states = hidden_states.reshape(-1, hidden_states.shape[-1])
+        if (hidden_states.dtype == torch.bfloat16 and self.weight.dtype == torch.bfloat16
+                and self.num_experts <= 256 and hidden_states.shape[-1] % 32 == 0):
+            w, ids = ops.router(hidden_states, self.weight, self.top_k, self.norm_topk_prob)
+            return w, ids, None
         router_logits = F.linear(hidden_states, self.weight)
         w, ids = ops.topk_softmax(router_logits, self.top_k, self.norm_topk_prob)
         return w, ids, None

@@ -48,6 +48,36 @@ def _(logits, top_k, renormalize):
             logits.new_empty(M, top_k, dtype=torch.int64))
 
 
+@torch.library.custom_op(f"{_NS}::router", mutates_args=())
+def router(hidden: torch.Tensor, gate_weight: torch.Tensor, top_k: int,
+           renormalize: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """TopKRouter.forward (moe.py:114-140) in one launch: bf16 logits =
+    hidden . gate_weight^T, fp32 softmax, top-k, optional renormalisation.
+    Returns (weights fp32 [T, k], ids int64 [T, k])."""
+    _lib.require_gpu(hidden)
+    hidden = hidden.reshape(-1, hidden.shape[-1]).contiguous()
+    gate_weight = gate_weight.contiguous()
+    if hidden.dtype != torch.bfloat16 or gate_weight.dtype != torch.bfloat16:
+        raise ValueError("router: hidden states and gate weight must be bfloat16")
+    M, H = hidden.shape
+    E = gate_weight.shape[0]
+    if gate_weight.shape[1] != H:
+        raise ValueError(f"router: gate weight {tuple(gate_weight.shape)} does not match hidden size {H}")
+    w = torch.empty(M, top_k, dtype=torch.float32, device=hidden.device)
+    ids = torch.empty(M, top_k, dtype=torch.int64, device=hidden.device)
+    check(load().mstar_moe_router(ptr(hidden), dtype_code(hidden.dtype), M, H, ptr(gate_weight), E,
+                                  top_k, int(renormalize), ptr(w), None, ptr(ids), None,
+                                  stream_of(hidden)), "router")
+    return w, ids
+
+
+@router.register_fake
+def _(hidden, gate_weight, top_k, renormalize):
+    M = hidden.numel() // hidden.shape[-1]
+    return (hidden.new_empty(M, top_k, dtype=torch.float32),
+            hidden.new_empty(M, top_k, dtype=torch.int64))
+
+
 @torch.library.custom_op(f"{_NS}::moe_align_block_size", mutates_args=())
 def moe_align_block_size(topk_ids: torch.Tensor, block_size: int,
                          num_experts: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
