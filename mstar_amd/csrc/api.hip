@@ -90,7 +90,9 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->stream = quant != MSTAR_QUANT_NONE && M <= kStreamMaxTokens &&
                stream_gemm_supported((int)H, (int)M, A_H16, bkind) &&
                stream_gemm_supported((int)I, (int)M, A_H16, bkind);
-  pl->ids_mode = pl->stream && quant == MSTAR_QUANT_FP8_W8A8 && pl->slots <= kStreamMaxIdsSlots;
+  pl->ids_mode = pl->stream && pl->slots <= kStreamMaxIdsSlots &&
+                 (quant == MSTAR_QUANT_FP8_W8A8 ||
+                  (quant == MSTAR_QUANT_W4A16 && H % 256 == 0 && I % 256 == 0));
   pl->bm = pl->stream ? 16 : choose_bm(pl->slots, E, quant == MSTAR_QUANT_FP8_W8A8);
   pl->max_padded = pl->slots + (int64_t)E * (pl->bm - 1);
   pl->max_blocks = (pl->max_padded + pl->bm - 1) / pl->bm;
@@ -107,7 +109,7 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   // With the router in the plan, the routing launch quantises the hidden
   // rows: widened to bf16 for the router-ids streaming kernel, as e4m3fn
   // codes for the tiled FP8 GEMM (multi-workgroup routing only).
-  pl->route_quant = with_route && ((pl->ids_mode && H % 512 == 0) ||
+  pl->route_quant = with_route && ((pl->ids_mode && quant == MSTAR_QUANT_FP8_W8A8 && H % 512 == 0) ||
                                    (quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream &&
                                     route_is_grid(M, top_k)));
   pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;

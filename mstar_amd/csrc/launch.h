@@ -121,6 +121,9 @@ bool stream_gemm_supported(int K, int max_rows, int akind, int bkind);
 
 // gemm_fp8.hip: 256 x 128 tile FP8 GEMM (8 waves, double-buffered LDS);
 // grouped needs the alignment block size 256.
+// W4A16 decode (router-ids mode): the CU-resident streaming kernel over
+// int4 weights (group-128 bf16 scales) and bf16 token rows.
+int launch_stream_int4_cu(const GemmArgs& a, int epi, hipStream_t stream);
 int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t stream);
 constexpr int kBigBlockM = 256;
 

@@ -417,6 +417,7 @@ __global__ __launch_bounds__(256) void stream_gemm_kernel(GemmArgs p) {
   extern __shared__ __align__(16) uint8_t smem[];
   uint8_t* sA = smem;
   float* sAs = (float*)(sA + PR * LDA);  // FP8: [PR][KS] group scales
+  __shared__ int sArow[PR];              // A row of each staged slot
 
   const int e = blockIdx.y, nt = blockIdx.x;
   const int cnt = p.expert_cnt[e];
@@ -497,11 +498,25 @@ __global__ __launch_bounds__(256) void stream_gemm_kernel(GemmArgs p) {
         }
       }
     } else {
+      // Row indices first, then eight independent 16-byte loads per thread
+      // in flight (one memory round trip per batch, not per chunk).
+      if (tid < rows) sArow[tid] = p.sorted_ids[off + r0 + tid] / p.top_k;
+      __syncthreads();
       const int chunks = rows * (K / 8);  // 16-byte chunks
-      for (int c = tid; c < chunks; c += 256) {
-        const int rr = c / (K / 8), cc = c % (K / 8);
-        const int arow = p.sorted_ids[off + r0 + rr] / p.top_k;
-        *(v4i*)(sA + rr * LDA + cc * 16) = *(const v4i*)(A16 + (int64_t)arow * p.lda + cc * 8);
+      constexpr int kB = 8;
+      for (int c0 = 0; c0 < chunks; c0 += 256 * kB) {
+        v4i v[kB];
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const int c = c0 + j * 256 + tid;
+          const int rr = c / (K / 8), cc = c % (K / 8);
+          v[j] = c < chunks ? *(const v4i*)(A16 + (int64_t)sArow[rr] * p.lda + cc * 8) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const int c = c0 + j * 256 + tid;
+          if (c < chunks) *(v4i*)(sA + (c / (K / 8)) * LDA + (c % (K / 8)) * 16) = v[j];
+        }
       }
     }
     __syncthreads();
@@ -632,6 +647,7 @@ int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dty
     return kInvalidArgument;
   }
   if (bkind == B_FP8BLK) return launch_stream_fp8(a, epi, kStreamExact, stream);
+  if (a.topk_ids) return launch_stream_int4_cu(a, epi, stream);
   return epi == EPI_ACT ? dispatch_ks<B_INT4G, EPI_ACT>(a, stream)
                         : dispatch_ks<B_INT4G, EPI_STORE>(a, stream);
 }

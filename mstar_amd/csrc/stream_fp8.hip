@@ -365,7 +365,9 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
 //    s_token[block] * s_weight[block].  Lane l ends with (weight rows
 //    4 (l/16) .. +3) x (token l % 16).  Lanes past the expert's token count
 //    read row 0 and store nothing (MFMA output columns are independent).
-enum : int { STAGE_Q16 = 0, STAGE_H16 = 1 };
+// STAGE_W4: W4A16 -- int4 weights (group-128 bf16 scales) and bf16 token
+// rows, staged as they are.
+enum : int { STAGE_Q16 = 0, STAGE_H16 = 1, STAGE_W4 = 2 };
 constexpr int kCuThreads = 512;
 constexpr int kCuWaves = kCuThreads / 64;
 constexpr int kCuRing = 3;        // ring slots per wave
@@ -394,16 +396,63 @@ __host__ __device__ inline size_t cu_rows_off(int E, int64_t M, int cap) {
   return (cu_sc_off<KS>(E, M) + (size_t)cap * (KS + 1) * 4 + 15) & ~(size_t)15;
 }
 
+// Wait for the oldest of `ahead` chunks in flight (DPC DMA instructions
+// each), leaving the younger ones -- two instructions fewer, for the
+// epilogue store or routed-weight load that may sit between them:
+// over-waiting is safe.
+template <int DPC, int N>
+__device__ __forceinline__ void wait_leaving_chunks(int ahead) {
+  if constexpr (N >= 2) {
+    if (ahead >= N) {
+      wait_vmcnt<((N - 1) * DPC - 2 > 0 ? (N - 1) * DPC - 2 : 0)>();
+      return;
+    }
+    wait_leaving_chunks<DPC, N - 1>(ahead);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+// Eight int4 codes (element j in bits 4j of w, stored as u = q + 8) as the
+// bf16 weights bf16((u - 8) * s): the nibbles spread into bytes (even
+// elements in lo, odd in hi), each byte converted exactly to fp32
+// (v_cvt_f32_ubyteN), fma(u, s, -8 s) (exact: (u - 8) s fits fp32), then
+// one rounding of each pair to bf16 (v_cvt_pk_bf16_f32) -- 23 VALU per 8.
+// The byte masks are opaque to the compiler, which would otherwise fold
+// them into per-nibble bit-field extracts.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v8s int4x8_dequant_bf16(uint32_t w, float s, float m8) {
+  uint32_t lo, hi;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
+  asm("v_lshrrev_b32 %0, 4, %1\n\tv_and_b32 %0, 0x0f0f0f0f, %0" : "=&v"(hi) : "v"(w));
+  v4i r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const f32x2 e = {__builtin_fmaf((float)((lo >> (8 * b)) & 0xffu), s, m8),
+                     __builtin_fmaf((float)((hi >> (8 * b)) & 0xffu), s, m8)};
+    r[b] = __builtin_bit_cast(int, __builtin_convertvector(e, bf16x2));
+  }
+  return __builtin_bit_cast(v8s, r);
+}
+
 template <int EPI, int KS, int STAGE>
 __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, int cap) {
+  constexpr bool W4 = STAGE == STAGE_W4;
+  static_assert(!W4 || KS % 2 == 0, "int4 chunks are two K-steps");
   constexpr int PITCH = cu_pitch<KS>();
-  constexpr int KC = cu_kc<KS>();
-  constexpr int CH = KS / KC;         // chunks per item
-  constexpr int SLOT = KC * 2048;     // ring slot bytes
-  constexpr int DPC = 2 * KC;         // DMA instructions per chunk
+  constexpr int KC = W4 ? 2 : cu_kc<KS>();  // K-steps per chunk
+  constexpr int CH = KS / KC;               // chunks per item
+  constexpr int WAVE_RING = kCuRing * cu_kc<KS>() * 2048;  // ring bytes per wave
+  // Ring slot: FP8 -- 16 rows x KC x 128 bytes; int4 -- 16 rows x KC x 64
+  // bytes, then the 16 rows' KC bf16 scales (4 bytes a row).
+  constexpr int SLOT = W4 ? KC * 1024 + 128 : KC * 2048;
+  constexpr int RING = WAVE_RING / SLOT;    // slots per wave
+  constexpr int DPC = W4 ? KC + 1 : 2 * KC;  // DMA instructions per chunk
+  static_assert(RING >= 3 && RING <= 6, "ring depth");
   constexpr int SPT = (int)(kStreamMaxIdsSlots / kCuThreads);  // router ids per thread
   // Waves that stage activation rows; the others prefetch weights meanwhile.
-  constexpr int SW = STAGE == STAGE_Q16 ? 2 : 4;
+  constexpr int SW = STAGE == STAGE_H16 ? 4 : 2;
   typedef __attribute__((address_space(3))) void* lds_void_ptr;
   extern __shared__ __align__(16) uint8_t smem[];
   const int E = p.num_experts;
@@ -421,7 +470,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   const int IPE = EPI == EPI_ACT ? p.inter / 8 : p.N / 16;  // items per expert
   const uint16_t* A16 = (const uint16_t*)p.A;
   uint16_t* C = (uint16_t*)p.C;
-  uint8_t* ring = smem + w * (kCuRing * SLOT);
+  uint8_t* ring = smem + w * WAVE_RING;
 
   // ---- prologue 1: per-expert counts and the active-expert mask.
   for (int e = tid; e < E; e += kCuThreads) sCnt[e] = 0;
@@ -468,6 +517,20 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   const int r8 = lane >> 3;
   const uint32_t lc16 = (uint32_t)(((lane & 7) ^ r8) * 16);
   auto dma_rows = [&](int e, int g, const uint8_t*& s0, const uint8_t*& s1) {
+    if constexpr (W4) {
+      // Lane l: item row l / 4, 16-byte piece l % 4 of a K-step's 64 bytes;
+      // lanes 0-15 also fetch item row l's scales.  Item rows 0-7 are gate
+      // rows and 8-15 the matching up rows (EPI_ACT).
+      auto row_of = [&](int rr) -> int {
+        if constexpr (EPI == EPI_ACT) return rr < 8 ? g * 8 + rr : p.inter + g * 8 + rr - 8;
+        else return g * 16 + rr;
+      };
+      const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride * 4;  // int32 words
+      s0 = Be + (int64_t)row_of(lane >> 2) * p.ldb * 4 + (lane & 3) * 16;
+      s1 = (const uint8_t*)((const uint16_t*)p.b_scale + (int64_t)e * p.bs_estride +
+                            (int64_t)row_of(lane & 15) * p.bs_ld);
+      return;
+    }
     const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride;
     int row0, row1;
     if constexpr (EPI == EPI_ACT) {
@@ -482,6 +545,16 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   };
   auto dma = [&](const uint8_t* s0, const uint8_t* s1, int c, int slot) {
     uint8_t* dst = ring + slot * SLOT;
+    if constexpr (W4) {
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk)
+        __builtin_amdgcn_global_load_lds((const void*)(s0 + (c * KC + kk) * 64),
+                                         (lds_void_ptr)(dst + kk * 1024), 16, 0, kDmaAux);
+      if (lane < 16)  // row lane's scales of K-steps c*KC, c*KC + 1
+        __builtin_amdgcn_global_load_lds((const void*)(s1 + c * KC * 2), (lds_void_ptr)(dst + KC * 1024),
+                                         4, 0, 0);
+      return;
+    }
 #pragma unroll
     for (int kk = 0; kk < KC; ++kk) {
       __builtin_amdgcn_global_load_lds((const void*)(s0 + (c * KC + kk) * 128),
@@ -500,7 +573,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
     const uint8_t *s0, *s1;
     dma_rows(active_expert(a), it_first - a * IPE, s0, s1);
 #pragma unroll
-    for (int c = 0; c < kCuRing - 1; ++c)
+    for (int c = 0; c < RING - 1; ++c)
       if (c < CH) dma(s0, s1, c, c);
   }
 
@@ -562,10 +635,11 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
         }
       }
     }
-    for (int i = tid; i < nrows * KS; i += ST) {
-      const int r = i / KS, ks = i - r * KS;
-      sSc[i] = p.a_scale[(int64_t)arow_of(r) * p.ld_as + ks];
-    }
+    if constexpr (!W4)  // token block scales (W4A16 rows are plain bf16)
+      for (int i = tid; i < nrows * KS; i += ST) {
+        const int r = i / KS, ks = i - r * KS;
+        sSc[i] = p.a_scale[(int64_t)arow_of(r) * p.ld_as + ks];
+      }
     wait_vmcnt<0>();
   };
   auto stage_quant = [&](int nrows, auto arow_of) {
@@ -643,7 +717,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
       return;
     }
     cc = ic;
-    // Issue the first kCuRing - 1 chunks (or adopt the prefetch).
+    // Issue the first RING - 1 chunks (or adopt the prefetch).
     int ahead = 0;      // chunks issued beyond the compute cursor
     int islot = 0;      // ring slot of the next issue
     const uint8_t *is0, *is1;
@@ -656,14 +730,14 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
         icur_r0 = ic.r0;
       }
       dma(is0, is1, ic.c, islot);
-      islot = islot + 1 == kCuRing ? 0 : islot + 1;
+      islot = islot + 1 == RING ? 0 : islot + 1;
       ++ahead;
       ihas = advance(ic);
     };
     const bool adopt = use_prefetch && ic.it == it_first && ic.c == 0;
     if (use_prefetch && !adopt) wait_vmcnt<0>();  // retire a prefetch this window does not use
     use_prefetch = false;
-    for (int n = 0; n < kCuRing - 1 && ihas; ++n) {
+    for (int n = 0; n < RING - 1 && ihas; ++n) {
       if (adopt) {  // already in flight
         if (ic.it != icur_it || ic.r0 != icur_r0) {
           const int a = ic.it / IPE;
@@ -672,7 +746,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
           icur_r0 = ic.r0;
         }
         if (ic.it != it_first || ic.r0 != cc.r0) break;  // the prefetch covered only the first unit
-        islot = islot + 1 == kCuRing ? 0 : islot + 1;
+        islot = islot + 1 == RING ? 0 : islot + 1;
         ++ahead;
         ihas = advance(ic);
       } else {
@@ -710,22 +784,34 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
       typedef const __attribute__((address_space(4))) float* const_fptr;
       const const_fptr bsc = (const_fptr)p.b_scale;
       v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+      v4f acc_w4[4] = {};  // W4: one accumulator per MFMA of a K-step (independent chains)
       const int unit_it = cc.it, unit_r0 = cc.r0;
       // ---- chunks of the unit
       while (true) {
-        while (ihas && ahead < kCuRing) issue_next();
+        while (ihas && ahead < RING) issue_next();
         // Wait for this chunk's DMA, leaving the later ones in flight (two
         // fewer, for the epilogue store / routed-weight load that may sit
         // between them: over-waiting is safe).
-        static_assert(kCuRing >= 3 && kCuRing <= 4, "waits below cover rings of 3 or 4 slots");
-        if (kCuRing >= 4 && ahead >= 4) wait_vmcnt<(3 * DPC - 2 > 0 ? 3 * DPC - 2 : 0)>();
-        else if (ahead >= 3) wait_vmcnt<(2 * DPC - 2 > 0 ? 2 * DPC - 2 : 0)>();
-        else if (ahead == 2) wait_vmcnt<(DPC - 2 > 0 ? DPC - 2 : 0)>();
-        else wait_vmcnt<0>();
+        wait_leaving_chunks<DPC, RING>(ahead);
         const uint8_t* wslot = ring + cslot * SLOT;
         // Wave-uniform, so the weight-scale reads below are scalar loads (a
         // vector load here would make the compiler drain the DMA queue).
         const int c = __builtin_amdgcn_readfirstlane(cc.c);
+        if constexpr (W4) {
+          // Row l16's group scales of both K-steps (the MFMA A row of this lane).
+          const uint32_t two = *(const uint32_t*)(wslot + KC * 1024 + l16 * 4);
+#pragma unroll
+          for (int kk = 0; kk < KC; ++kk) {
+            const int ks = c * KC + kk;
+            const float sr = bf16_bits_to_f32((uint16_t)(kk == 0 ? two & 0xffffu : two >> 16));
+            const float m8 = -8.f * sr;
+            const v4i wq = *(const v4i*)(wslot + kk * 1024 + l16 * 64 + lg * 16);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+              acc_w4[m] = mfma_bf16_16x16x32(int4x8_dequant_bf16((uint32_t)wq[m], sr, m8),
+                                             *(const v8s*)(trow + ks * 256 + m * 16), acc_w4[m]);
+          }
+        } else {
 #pragma unroll
         for (int kk = 0; kk < KC; ++kk) {
           const int ks = c * KC + kk;
@@ -744,10 +830,12 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
           t = mfma_bf16_16x16x32(fp8x8_to_bf16x8(whi[2], whi[3]), *(const v8s*)(trow + ks * 256 + 48), t);
           acc += t * f;
         }
-        cslot = cslot + 1 == kCuRing ? 0 : cslot + 1;
+        }
+        cslot = cslot + 1 == RING ? 0 : cslot + 1;
         --ahead;
         const bool more = advance(cc);
         if (!more || cc.it != unit_it || cc.r0 != unit_r0) {
+          if constexpr (W4) acc = (acc_w4[0] + acc_w4[1]) + (acc_w4[2] + acc_w4[3]);
           // ---- epilogue of the unit: lane (l16, lg) holds weight rows 4 lg + r for token l16.
           if constexpr (EPI == EPI_ACT) {
             // Gate rows 0-7 sit in lanes lg 0-1, the matching up rows 32 lanes up.
@@ -819,6 +907,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
     if (w < SW) {
       const auto arow_of = [&](int j) { return sList[lbase + j] / p.top_k; };
       if constexpr (STAGE == STAGE_Q16) stage_copy_q16(nrows, arow_of);
+      else if constexpr (STAGE == STAGE_W4) stage_copy_q16(nrows, arow_of);
       else stage_quant(nrows, arow_of);
       if (EPI != EPI_ACT && p.mul_routed)
         for (int j = tid; j < nrows; j += ST)
@@ -891,9 +980,11 @@ static int run_stream_fp8_cu(const GemmArgs& a, int cap, size_t shmem, hipStream
 // The CU-resident kernel for (exact, router-ids mode), or false if the shape
 // does not fit it.
 template <int KS>
-static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, int* status) {
+static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, int* status,
+                              bool int4 = false) {
   const size_t per_row = (size_t)cu_pitch<KS>() + (KS + 1) * 4;
   if (a.a_scale && !a.a_q16) return false;  // e4m3fn rows: the LDS-staged kernel
+  if (int4 && (KS % 2 != 0 || a.a_scale)) return false;
   // Rows staged per window: as many as the LDS budget allows.
   // 1 KB stays free for the kernel's static LDS.
   const size_t fixed = cu_sc_off<KS>(a.num_experts, a.M) + 16 + 1024;
@@ -901,6 +992,13 @@ static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, in
   int cap = (int)((kCuLdsMax - fixed) / per_row);
   if (cap > 1024) cap = 1024;
   const size_t shmem = cu_rows_off<KS>(a.num_experts, a.M, cap) + (size_t)cap * cu_pitch<KS>();
+  if constexpr (KS % 2 == 0) {
+    if (int4) {
+      *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_W4>(a, cap, shmem, stream)
+                               : run_stream_fp8_cu<EPI_STORE, KS, STAGE_W4>(a, cap, shmem, stream);
+      return true;
+    }
+  }
   if (a.a_q16)
     *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_Q16>(a, cap, shmem, stream)
                              : run_stream_fp8_cu<EPI_STORE, KS, STAGE_Q16>(a, cap, shmem, stream);
@@ -908,6 +1006,30 @@ static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, in
     *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_H16>(a, cap, shmem, stream)
                              : run_stream_fp8_cu<EPI_STORE, KS, STAGE_H16>(a, cap, shmem, stream);
   return true;
+}
+
+int launch_stream_int4_cu(const GemmArgs& a, int epi, hipStream_t stream) {
+  if (!a.topk_ids || a.M > kStreamMaxIdsSlots || a.num_experts > 1024 || a.K % 256 != 0 ||
+      (epi == EPI_ACT ? a.inter % 8 != 0 : a.N % 16 != 0)) {
+    set_last_error("stream_int4: needs router ids, at most %lld slots, K %% 256 == 0",
+                   (long long)kStreamMaxIdsSlots);
+    return kUnsupported;
+  }
+  int st = kOk;
+  bool done = false;
+  switch (a.K / 128) {
+    case 2: done = try_stream_fp8_cu<2>(a, epi, stream, &st, true); break;
+    case 4: done = try_stream_fp8_cu<4>(a, epi, stream, &st, true); break;
+    case 6: done = try_stream_fp8_cu<6>(a, epi, stream, &st, true); break;
+    case 8: done = try_stream_fp8_cu<8>(a, epi, stream, &st, true); break;
+    case 12: done = try_stream_fp8_cu<12>(a, epi, stream, &st, true); break;
+    case 16: done = try_stream_fp8_cu<16>(a, epi, stream, &st, true); break;
+  }
+  if (!done) {
+    set_last_error("stream_int4: unsupported shape (K=%d)", a.K);
+    return kUnsupported;
+  }
+  return st;
 }
 
 bool stream_fp8_supported(int K, int N, int inter, int epi) {
