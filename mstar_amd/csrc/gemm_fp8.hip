@@ -96,6 +96,13 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     return j * G + r;
   };
   if (tile_of(0) >= total) return;
+  // Tile t -> (m-block, n-tile).  Grouped: m-block major, so an XCD's
+  // consecutive tiles are the n-tiles of a few m-blocks (shared A rows; the
+  // m-blocks of one expert share weights).  Dense: m-block minor, so they
+  // are the m-blocks of a few n-tiles and each weight tile is read from HBM
+  // once (the A rows, m_valid x K, stay in L2 / the last-level cache).
+  auto mb_of = [&](int t) -> int { return GROUPED ? t / n_tiles : t % m_valid; };
+  auto nt_of = [&](int t) -> int { return GROUPED ? t % n_tiles : t / m_valid; };
   const int KB = p.K / 128;
 
   // ---- tile metadata: grouped tiles take their slots from sorted_ids by
@@ -103,7 +110,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   auto issue_ids = [&](int t, int buf) {
     if constexpr (GROUPED) {
       if (t < total && wave >= 4) {
-        const int mb = t / n_tiles;
+        const int mb = mb_of(t);
         __builtin_amdgcn_global_load_lds((const void*)(p.sorted_ids + (int64_t)mb * BM + (wave - 4) * 64 + lane),
                                          (lds_void_ptr)(sMeta + buf * kBigMetaInts + (wave - 4) * 64), 4, 0, 0);
       }
@@ -115,7 +122,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
       const int s = sMeta[buf * kBigMetaInts + r];
       return s < p.M ? s : -1;
     } else {
-      const int64_t m = (int64_t)(t / n_tiles) * BM + r;
+      const int64_t m = (int64_t)mb_of(t) * BM + r;
       return m < p.M ? (int)m : -1;
     }
   };
@@ -130,7 +137,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   uint32_t a_off[AI], b_off[BI];
   const float* sc_src = nullptr;
   auto setup_issue = [&](int t, int buf) {
-    const int mb = t / n_tiles, nt = t - mb * n_tiles;
+    const int mb = mb_of(t), nt = nt_of(t);
     int expert = 0;
     // Constant address space: a scalar load (a vector load here would make
     // the compiler drain the DMA queue to use it).
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
 
   for (int j = 0; tile_of(j) < total; ++j) {
     const int t = tile_of(j);
-    const int mb = t / n_tiles, nt = t - mb * n_tiles;
+    const int mb = mb_of(t), nt = nt_of(t);
     const int buf = j % kBigIdBufs;
     // acc[i][j]: the transposed 32x32 tile (weight rows x token columns).
     v16f acc[MB][NB];
