@@ -431,8 +431,8 @@ int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, 
     set_last_error("topk_softmax: hidden quantisation needs H %% 512 == 0 (H=%lld)", (long long)H);
     return kInvalidArgument;
   }
-  if (M < 0 || E <= 0 || E > 1024 || k <= 0 || k > 64 || k > E || !w || (!ids32 && !ids64) ||
-      (M > 0 && !logits)) {
+  if (M < 0 || E <= 0 || E > 1024 || k <= 0 || k > 64 || k > E ||
+      (M > 0 && (!logits || !w || (!ids32 && !ids64)))) {
     set_last_error("topk_softmax: invalid arguments (M=%lld E=%d k=%d)", (long long)M, E, k);
     return kInvalidArgument;
   }
@@ -618,7 +618,7 @@ int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, 
                  int32_t* expert_ids, int32_t* ntpp, int64_t max_padded, int32_t* expert_off,
                  int32_t* expert_cnt, void* scratch, size_t scratch_bytes, hipStream_t stream,
                  const void* hidden, int64_t H, uint8_t* hq, float* hs) {
-  if (M < 0 || k <= 0 || k > 64 || k > E || !w || (M > 0 && !logits)) {
+  if (M < 0 || k <= 0 || k > 64 || k > E || (M > 0 && (!logits || !w))) {
     set_last_error("moe_route: invalid arguments (M=%lld E=%d k=%d)", (long long)M, E, k);
     return kInvalidArgument;
   }

@@ -85,7 +85,7 @@ int launch_router(const void* hidden, int64_t M, int64_t H, const void* gate_wei
                   int renorm, float* w, int32_t* ids32, int64_t* ids64, void* logits_out,
                   hipStream_t stream) {
   if (M < 0 || H <= 0 || H % 32 != 0 || H > INT32_MAX || E <= 0 || E > kRouterMaxE || k <= 0 ||
-      k > E || k > 64 || !w || (!ids32 && !ids64) || (M > 0 && (!hidden || !gate_weight))) {
+      k > E || k > 64 || (M > 0 && (!w || (!ids32 && !ids64) || !hidden || !gate_weight))) {
     set_last_error("router: invalid arguments (M=%lld H=%lld E=%d k=%d; H %% 32 == 0, E <= %d)",
                    (long long)M, (long long)H, E, k, kRouterMaxE);
     return kInvalidArgument;
