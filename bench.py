@@ -18,6 +18,10 @@ The JSON line also carries:
   launch stream;
 * prefill -- config 3 at M=8192 (Zipf-biased routing): us/layer, TFLOP/s and
   the fraction of dense FP8 peak;
+* dense_fp8 -- config 4: the W8A8 dense GEMM (per-token x per-channel
+  scales) at M=32 and M=4096 with N=151936 (the LM-head shape);
+* w4a16 -- config 5: the decode layer with int4 group-128 weights at M=32
+  and M=1024;
 * cpu_baseline -- the reference's CPU MoE path (TopKRouter + the per-expert
   dispatch of mstar/model/components/moe.py:131-185, restated in oracle/)
   on a bounded sample of the same workload, on this host's cores.
@@ -39,6 +43,7 @@ import torch  # noqa: E402
 H, E, K_TOP, INTER = 2048, 128, 8, 768
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 EXPERT_FP8_BYTES = 2 * INTER * H + H * INTER                      # 4,718,592
 EXPERT_SCALE_BYTES = ((2 * INTER // 128) * (H // 128) + (H // 128) * (INTER // 128)) * 4  # 1,152
 W_COPIES = 4
@@ -63,6 +68,7 @@ def parse():
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--no-extra", action="store_true", help="skip the config 4 / 5 lines")
     p.add_argument("--kernel-only", action="store_true",
                    help="launch only the gate_up GEMM in a loop (for profiler runs)")
     return p.parse_args()
@@ -172,6 +178,60 @@ def gate_up_kernel_timing(x, logits, weights, steps, warmup):
     end.record(stream)
     end.synchronize()
     return start.elapsed_time(end) * 1e3 / steps  # us
+
+
+def dense_fp8_lines(args, N=151936, K=2048):
+    """Config 4: y = bf16((A_q . W_q^T) s_a s_w), A per-token and W per-channel
+    e4m3fn (mstar_fp8_scaled_mm), one graph replay per step."""
+    from mstar_amd import ops, quant
+    g = torch.Generator(device="cuda").manual_seed(7)
+    wq, ws = quant.quantize_fp8_per_channel(torch.randn(N, K, generator=g, device="cuda") * 0.02)
+    res = {}
+    for Md in (32, 4096):
+        a = torch.randn(Md, K, generator=g, device="cuda").to(torch.bfloat16)
+        aq, sa = ops.quant_fp8_per_token(a)
+        gr, _ = capture(lambda: ops.fp8_scaled_mm(aq, sa, wq, ws))
+        sec = time_graphs([gr], 50 if Md == 32 else 20, 5)
+        byts = N * K + Md * K + N * 4 + Md * 4 + Md * N * 2
+        tf = 2.0 * Md * N * K / sec / 1e12
+        res[f"M{Md}"] = {"us": round(sec * 1e6, 1), "GBps": round(byts / sec / 1e9, 1),
+                         "hbm_frac": round(byts / sec / 1e9 / HBM_PEAK_GBS, 4), "TFLOPs": round(tf, 1),
+                         "mfma_fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4)}
+        del gr
+    res["workload"] = f"config 4: [M, {K}] x [{N}, {K}]^T, per-token x per-channel e4m3fn"
+    return res
+
+
+def w4a16_lines(args):
+    """Config 5: the decode layer with int4 group-128 weights (bf16 scales),
+    routing from logits, two rotated weight copies."""
+    from mstar_amd import _lib, ops, quant
+    g = torch.Generator(device="cuda").manual_seed(9)
+    w1 = torch.randn(E, 2 * INTER, H, generator=g, device="cuda") * 0.02
+    w2 = torch.randn(E, H, INTER, generator=g, device="cuda") * 0.02
+    copies = [quant.quantize_int4_group(w1) + quant.quantize_int4_group(w2)]
+    del w1, w2
+    copies.append(tuple(t.clone() for t in copies[0]))
+    per_expert = 2 * INTER * H // 2 + H * INTER // 2 + (2 * INTER * (H // 128) + H * (INTER // 128)) * 2
+    res = {}
+    for Mw in (32, 1024):
+        x, logits = make_inputs(Mw, bias=False, seed=11)
+        grs = []
+        for p1, t1, p2, t2 in copies:
+            gr, _ = capture(lambda p1=p1, t1=t1, p2=p2, t2=t2: ops.moe_layer(
+                x, logits, p1, p2, K_TOP, True, 0, _lib.QUANT_W4A16, t1, t2)[0])
+            grs.append(gr)
+        sec = time_graphs(grs, 50, 5)
+        hits = n_hit(logits)
+        byts = hits * per_expert + Mw * H * 4 + Mw * E * 4
+        tf = 2.0 * Mw * K_TOP * EXPERT_FP8_BYTES / sec / 1e12
+        res[f"M{Mw}"] = {"us": round(sec * 1e6, 1), "hit_experts": hits,
+                         "GBps": round(byts / sec / 1e9, 1),
+                         "hbm_frac": round(byts / sec / 1e9 / HBM_PEAK_GBS, 4),
+                         "TFLOPs": round(tf, 1), "mfma_bf16_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+        del grs
+    res["workload"] = "config 5: MoE layer, int4 group-128 weights, bf16 activations"
+    return res
 
 
 def cpu_baseline(weights, M, seconds):
@@ -285,6 +345,12 @@ def main():
                           "mfma_fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4),
                           "workload": "config 3: Zipf-biased routing, same weights"}
         del gp
+
+    if not args.no_extra:
+        del weights, graphs
+        torch.cuda.empty_cache()
+        out["dense_fp8"] = dense_fp8_lines(args)
+        out["w4a16"] = w4a16_lines(args)
 
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(base, M, args.cpu_seconds)
