@@ -236,6 +236,29 @@ __device__ inline int wave_incl_scan(int v) {
 // Lane 63's value, wave-uniform (a scalar read, no LDS round trip).
 __device__ inline int wave_last(int v) { return __builtin_amdgcn_readlane(v, 63); }
 
+// Eight int4 codes (element j in bits 4j of w, stored as u = q + 8) as the
+// bf16 weights bf16((u - 8) * s): the nibbles spread into bytes (even
+// elements in lo, odd in hi), each byte converted exactly to fp32
+// (v_cvt_f32_ubyteN), fma(u, s, -8 s) (exact: (u - 8) s fits fp32), then
+// one rounding of each pair to bf16 (v_cvt_pk_bf16_f32) -- 23 VALU per 8.
+// The byte masks are opaque to the compiler, which would otherwise fold
+// them into per-nibble bit-field extracts.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v8s int4x8_dequant_bf16(uint32_t w, float s, float m8) {
+  uint32_t lo, hi;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
+  asm("v_lshrrev_b32 %0, 4, %1\n\tv_and_b32 %0, 0x0f0f0f0f, %0" : "=&v"(hi) : "v"(w));
+  v4i r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const f32x2 e = {__builtin_fmaf((float)((lo >> (8 * b)) & 0xffu), s, m8),
+                     __builtin_fmaf((float)((hi >> (8 * b)) & 0xffu), s, m8)};
+    r[b] = __builtin_bit_cast(int, __builtin_convertvector(e, bf16x2));
+  }
+  return __builtin_bit_cast(v8s, r);
+}
+
 // ---------------------------------------------------------------- MFMA
 // 16x16x128 FP8 (e4m3fn x e4m3fn), fp32 accumulate.  Operand layout (both A
 // and B): lane l supplies row/column (l % 16) and 32 consecutive K bytes at

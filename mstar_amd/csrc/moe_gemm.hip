@@ -46,6 +46,7 @@ __device__ inline v8i load_v8i_a16(const uint8_t* p) {
 // 8 int4 nibbles (u = q + 8) -> 8 16-bit values bf16/fp16(q * s).
 template <int DT>
 __device__ inline v8s dequant_int4x8(uint32_t word, float s) {
+  if constexpr (DT == kBF16) return int4x8_dequant_bf16(word, s, -8.f * s);
   v8s r;
 #pragma unroll
   for (int n = 0; n < 8; ++n) {

@@ -413,29 +413,6 @@ __device__ __forceinline__ void wait_leaving_chunks(int ahead) {
   }
 }
 
-// Eight int4 codes (element j in bits 4j of w, stored as u = q + 8) as the
-// bf16 weights bf16((u - 8) * s): the nibbles spread into bytes (even
-// elements in lo, odd in hi), each byte converted exactly to fp32
-// (v_cvt_f32_ubyteN), fma(u, s, -8 s) (exact: (u - 8) s fits fp32), then
-// one rounding of each pair to bf16 (v_cvt_pk_bf16_f32) -- 23 VALU per 8.
-// The byte masks are opaque to the compiler, which would otherwise fold
-// them into per-nibble bit-field extracts.
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ v8s int4x8_dequant_bf16(uint32_t w, float s, float m8) {
-  uint32_t lo, hi;
-  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(lo) : "v"(w));
-  asm("v_lshrrev_b32 %0, 4, %1\n\tv_and_b32 %0, 0x0f0f0f0f, %0" : "=&v"(hi) : "v"(w));
-  v4i r;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const f32x2 e = {__builtin_fmaf((float)((lo >> (8 * b)) & 0xffu), s, m8),
-                     __builtin_fmaf((float)((hi >> (8 * b)) & 0xffu), s, m8)};
-    r[b] = __builtin_bit_cast(int, __builtin_convertvector(e, bf16x2));
-  }
-  return __builtin_bit_cast(v8s, r);
-}
-
 template <int EPI, int KS, int STAGE>
 __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, int cap) {
   constexpr bool W4 = STAGE == STAGE_W4;
