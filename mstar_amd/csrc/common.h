@@ -82,16 +82,9 @@ __device__ inline int cvt_fp8x4(float a, float b, float c, float d) {
 __device__ inline float clamp_fp8(float x) { return fminf(fmaxf(x, -kFp8Max), kFp8Max); }
 
 // ------------------------------------------------------------ wave helpers
-__device__ inline int lane_id() { return __lane_id(); }
-
 __device__ inline float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
 // Max over aligned groups of `W` lanes (W a power of two <= 64).
