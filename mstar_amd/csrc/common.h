@@ -252,6 +252,17 @@ __device__ __forceinline__ v8s int4x8_dequant_bf16(uint32_t w, float s, float m8
   return __builtin_bit_cast(v8s, r);
 }
 
+// Eight int4 codes (element j in bits 4j of w) as bf16 128 + u, two per
+// dword in the order 0, 4, 1, 5, 2, 6, 3, 7: 128 + u is bf16 0x4300 | u, so
+// each pair is one shift and one and-or.  A dot product over these values
+// is sum (u + 128) x; sum (u - 8) x follows by subtracting 136 sum x.
+__device__ __forceinline__ v8s int4x8_bias128(uint32_t w) {
+  v4i r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r[j] = (int)(((w >> (4 * j)) & 0x000F000Fu) | 0x43004300u);
+  return __builtin_bit_cast(v8s, r);
+}
+
 // ---------------------------------------------------------------- MFMA
 // 16x16x128 FP8 (e4m3fn x e4m3fn), fp32 accumulate.  Operand layout (both A
 // and B): lane l supplies row/column (l % 16) and 32 consecutive K bytes at

@@ -365,8 +365,10 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
 //    s_token[block] * s_weight[block].  Lane l ends with (weight rows
 //    4 (l/16) .. +3) x (token l % 16).  Lanes past the expert's token count
 //    read row 0 and store nothing (MFMA output columns are independent).
-// STAGE_W4: W4A16 -- int4 weights (group-128 bf16 scales) and bf16 token
-// rows, staged as they are.
+// STAGE_W4: W4A16 -- int4 weights (group-128 bf16 scales whose products
+// with the codes are exact in bf16) and bf16 token rows, staged with each
+// group of 8 reordered to the codes' unpacked order (int4x8_bias128) and
+// with each 128-element block's sum.
 enum : int { STAGE_Q16 = 0, STAGE_H16 = 1, STAGE_W4 = 2 };
 constexpr int kCuThreads = 512;
 constexpr int kCuWaves = kCuThreads / 64;
@@ -429,7 +431,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   static_assert(RING >= 3 && RING <= 6, "ring depth");
   constexpr int SPT = (int)(kStreamMaxIdsSlots / kCuThreads);  // router ids per thread
   // Waves that stage activation rows; the others prefetch weights meanwhile.
-  constexpr int SW = STAGE == STAGE_H16 ? 4 : 2;
+  constexpr int SW = STAGE == STAGE_Q16 ? 2 : 4;
   typedef __attribute__((address_space(3))) void* lds_void_ptr;
   extern __shared__ __align__(16) uint8_t smem[];
   const int E = p.num_experts;
@@ -612,7 +614,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
         }
       }
     }
-    if constexpr (!W4)  // token block scales (W4A16 rows are plain bf16)
+    if constexpr (!W4)  // token block scales
       for (int i = tid; i < nrows * KS; i += ST) {
         const int r = i / KS, ks = i - r * KS;
         sSc[i] = p.a_scale[(int64_t)arow_of(r) * p.ld_as + ks];
@@ -645,6 +647,45 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
         }
       }
     }
+  };
+
+  // W4: token rows as bf16, each group of 8 reordered to 0, 4, 1, 5, 2, 6,
+  // 3, 7, and the fp32 sum of each 128-element block into sSc.
+  auto stage_w4 = [&](int nrows, auto arow_of) {
+    constexpr int B = 8;
+    const int groups = nrows * KS;
+    for (int g0 = 0; g0 < groups; g0 += (ST / 16) * B) {
+      v4i raw[B];
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        const int gq = g0 + j * (ST / 16) + (tid >> 4), sub = tid & 15;
+        const bool live = gq < groups;
+        const int r = live ? gq / KS : 0, ks = live ? gq - (gq / KS) * KS : 0;
+        raw[j] = live ? *(const v4i*)(A16 + (int64_t)arow_of(r) * p.lda + ks * 128 + sub * 8)
+                      : v4i{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        const int gq = g0 + j * (ST / 16) + (tid >> 4), sub = tid & 15;
+        const bool live = gq < groups;
+        const int r = live ? gq / KS : 0, ks = live ? gq - (gq / KS) * KS : 0;
+        const uint32_t d0 = raw[j][0], d1 = raw[j][1], d2 = raw[j][2], d3 = raw[j][3];
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t d = (uint32_t)raw[j][i];
+          sum += bf16_bits_to_f32((uint16_t)(d & 0xffffu)) + bf16_bits_to_f32((uint16_t)(d >> 16));
+        }
+        sum = row_fsum16(sum);  // the 16 lanes of a block are one DPP row
+        if (live) {
+          const v4i o = v4i{(int)((d0 & 0xffffu) | (d2 << 16)), (int)((d0 >> 16) | (d2 & 0xffff0000u)),
+                            (int)((d1 & 0xffffu) | (d3 << 16)), (int)((d1 >> 16) | (d3 & 0xffff0000u))};
+          *(v4i*)(sRows + r * PITCH + ks * 256 + sub * 16) = o;
+          if (sub == 0) sSc[r * KS + ks] = sum;
+        }
+      }
+    }
+    wait_vmcnt<0>();
   };
 
   // ---- the wave's units in a window: (item, pass of up to 16 rows).  A
@@ -761,7 +802,6 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
       typedef const __attribute__((address_space(4))) float* const_fptr;
       const const_fptr bsc = (const_fptr)p.b_scale;
       v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-      v4f acc_w4[4] = {};  // W4: one accumulator per MFMA of a K-step (independent chains)
       const int unit_it = cc.it, unit_r0 = cc.r0;
       // ---- chunks of the unit
       while (true) {
@@ -775,18 +815,27 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
         // vector load here would make the compiler drain the DMA queue).
         const int c = __builtin_amdgcn_readfirstlane(cc.c);
         if constexpr (W4) {
-          // Row l16's group scales of both K-steps (the MFMA A row of this lane).
-          const uint32_t two = *(const uint32_t*)(wslot + KC * 1024 + l16 * 4);
+          // Scales of rows 4 lg .. +3 (the rows this lane's results belong
+          // to) for both K-steps: 16 contiguous bytes.
+          const v4i sc4 = *(const v4i*)(wslot + KC * 1024 + lg * 16);
 #pragma unroll
           for (int kk = 0; kk < KC; ++kk) {
             const int ks = c * KC + kk;
-            const float sr = bf16_bits_to_f32((uint16_t)(kk == 0 ? two & 0xffffu : two >> 16));
-            const float m8 = -8.f * sr;
             const v4i wq = *(const v4i*)(wslot + kk * 1024 + l16 * 64 + lg * 16);
+            v4f t = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int m = 0; m < 4; ++m)
-              acc_w4[m] = mfma_bf16_16x16x32(int4x8_dequant_bf16((uint32_t)wq[m], sr, m8),
-                                             *(const v8s*)(trow + ks * 256 + m * 16), acc_w4[m]);
+              t = mfma_bf16_16x16x32(int4x8_bias128((uint32_t)wq[m]), *(const v8s*)(trow + ks * 256 + m * 16), t);
+            // sum (u - 8) x = sum (u + 128) x - 136 sum x, then the row's scale
+            // (q * s is exact in bf16, so scaling after the sum is the
+            // bf16(q * s) weight's product).
+            const float bias = 136.f * tsc[ks];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const uint32_t two = (uint32_t)sc4[r];
+              const float sr = bf16_bits_to_f32((uint16_t)(kk == 0 ? two & 0xffffu : two >> 16));
+              acc[r] += (t[r] - bias) * sr;
+            }
           }
         } else {
 #pragma unroll
@@ -812,7 +861,6 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
         --ahead;
         const bool more = advance(cc);
         if (!more || cc.it != unit_it || cc.r0 != unit_r0) {
-          if constexpr (W4) acc = (acc_w4[0] + acc_w4[1]) + (acc_w4[2] + acc_w4[3]);
           // ---- epilogue of the unit: lane (l16, lg) holds weight rows 4 lg + r for token l16.
           if constexpr (EPI == EPI_ACT) {
             // Gate rows 0-7 sit in lanes lg 0-1, the matching up rows 32 lanes up.
@@ -884,7 +932,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
     if (w < SW) {
       const auto arow_of = [&](int j) { return sList[lbase + j] / p.top_k; };
       if constexpr (STAGE == STAGE_Q16) stage_copy_q16(nrows, arow_of);
-      else if constexpr (STAGE == STAGE_W4) stage_copy_q16(nrows, arow_of);
+      else if constexpr (STAGE == STAGE_W4) stage_w4(nrows, arow_of);
       else stage_quant(nrows, arow_of);
       if (EPI != EPI_ACT && p.mul_routed)
         for (int j = tid; j < nrows; j += ST)

@@ -13,9 +13,12 @@ branches were stripped, mstar/utils/fused_moe/kernels.py:3-7):
   reciprocal, which can be one ulp off), so the codes do not depend on the
   device the weights are quantised on.
 * FP8 per-channel: one scale per output row, same rule.
-* int4 group-128: ``s = bf16(max(amax, 1e-10)/7)`` per 128 of K,
-  ``q = clamp(round(w / s), -8, 7)``, stored as ``u = q + 8`` nibbles, eight
-  per int32, element ``k`` in bits ``4*(k % 8)`` of word ``k // 8``.
+* int4 group-128: ``s = max(amax, 1e-10)/7`` rounded up to five significant
+  bits (exact in bf16) per 128 of K, ``q = round(w / s)`` (within [-7, 7]),
+  stored as ``u = q + 8`` nibbles, eight per int32, element ``k`` in bits
+  ``4*(k % 8)`` of word ``k // 8``.  With five significant bits in ``s`` and
+  at most three in ``q``, every dequantised weight ``q * s`` is exact in
+  bf16, so a kernel may apply the scale after its dot products.
 """
 from __future__ import annotations
 
@@ -34,6 +37,14 @@ def _div(a: torch.Tensor, b) -> torch.Tensor:
     fp32 operands, rounded once)."""
     b = b.double() if torch.is_tensor(b) else float(b)
     return (a.double() / b).float()
+
+
+def round_up_5bits(x: torch.Tensor) -> torch.Tensor:
+    """Positive fp32 ``x`` rounded up to five significant bits (four mantissa
+    bits): the smallest such value >= x."""
+    bits = x.float().contiguous().view(torch.int32)
+    step = 1 << (23 - 4)
+    return ((bits + (step - 1)) & ~(step - 1)).view(torch.float32)
 
 
 @torch.no_grad()
@@ -68,7 +79,7 @@ def quantize_int4_group(w: torch.Tensor, group: int = 128):
     if K % group or K % 8:
         raise ValueError(f"quantize_int4_group: K={K} must be a multiple of {group} and 8")
     wf = w.float().view(*lead, N, K // group, group)
-    s = _div(wf.abs().amax(dim=-1).clamp_min(EPS), 7.0).to(torch.bfloat16)
+    s = round_up_5bits(_div(wf.abs().amax(dim=-1).clamp_min(EPS), 7.0)).to(torch.bfloat16)
     q = torch.round(_div(wf, s.float()[..., None])).clamp(-8, 7).to(torch.int32).view(*lead, N, K)
     u = (q + 8).view(*lead, N, K // 8, 8)
     packed = torch.zeros(*lead, N, K // 8, dtype=torch.int32, device=w.device)

@@ -37,6 +37,8 @@ Pinning status (how each function is checked by ``tests/test_oracle.py``):
 from __future__ import annotations
 
 import numpy as np
+import math
+
 import torch
 import torch.nn.functional as F
 
@@ -329,18 +331,28 @@ def fp8_scaled_mm(a_q, a_s, w_q, w_s, out_dtype=torch.bfloat16):
     return (acc * a_s[:, None] * w_s[None, :]).to(out_dtype)
 
 
+def _ceil_5_significant_bits(x: float) -> float:
+    """Smallest value >= x (x > 0) with five significant binary digits, by
+    frexp: x = m * 2^e, m in [0.5, 1); keep ceil(m * 32) / 32."""
+    m, e = math.frexp(x)
+    return math.ldexp(math.ceil(m * 32.0) / 32.0, e)
+
+
 def quant_int4_group(w: torch.Tensor, group: int = 128):
     """Symmetric int4, one bf16 scale per ``group`` along K:
-    ``s = bf16(max(amax, eps) / 7)``, ``q = clamp(round_half_even(w / s),
-    -8, 7)``.  Packing: nibble ``u = q + 8``; element ``k`` sits in bits
-    ``4*(k % 8)`` of int32 word ``k // 8`` (little-endian nibble order).
-    ``w`` is ``[..., N, K]``; returns ``(packed int32 [..., N, K/8],
-    scales bf16 [..., N, K/group])``."""
+    ``s = ceil_5bits(max(amax, eps) / 7)`` (five significant bits, exact in
+    bf16), ``q = round_half_even(w / s)`` (|q| <= 7 since s >= amax/7).
+    Packing: nibble ``u = q + 8``; element ``k`` sits in bits ``4*(k % 8)``
+    of int32 word ``k // 8`` (little-endian nibble order).  ``w`` is
+    ``[..., N, K]``; returns ``(packed int32 [..., N, K/8], scales bf16
+    [..., N, K/group])``."""
     *lead, N, K = w.shape
     assert K % group == 0 and K % 8 == 0
     wf = w.float().view(*lead, N, K // group, group)
     amax = wf.abs().amax(dim=-1).clamp_min(QUANT_EPS)
-    s = (amax / 7.0).to(torch.bfloat16)
+    q7 = (amax.double() / 7.0).float()  # the fp32 quotient, correctly rounded
+    s = torch.tensor([_ceil_5_significant_bits(v) for v in q7.flatten().tolist()],
+                     dtype=torch.float32).view(q7.shape).to(torch.bfloat16)
     q = torch.round(wf / s.float()[..., None]).clamp(-8, 7).to(torch.int64).view(*lead, N, K)
     u = (q + 8).view(*lead, N, K // 8, 8)
     shifts = torch.arange(8, dtype=torch.int64) * 4
@@ -359,7 +371,8 @@ def unpack_int4(packed: torch.Tensor):
 
 
 def dequant_int4_group(packed, scales, group=128):
-    """``w = bf16(q * s)`` -- the bf16 weight the W4A16 GEMM multiplies."""
+    """``w = bf16(q * s)`` -- the bf16 weight the W4A16 GEMM multiplies (exact:
+    ``q * s`` needs at most eight significant bits)."""
     q = unpack_int4(packed).float()
     s = scales.float().repeat_interleave(group, dim=-1)
     return (q * s).to(torch.bfloat16)

@@ -307,12 +307,23 @@ def test_int4_pack_roundtrip_and_layout():
     word = int(packed[1, 2, 5]) & 0xFFFFFFFF
     for n in range(8):
         assert ((word >> (4 * n)) & 0xF) - 8 == int(q[1, 2, 5 * 8 + n])
-    # Symmetric rounding: q = round(w / s) with s = bf16(amax / 7).
+    # Scale: the first value >= amax/7 with five significant bits (checked
+    # by brute force over the 16 five-bit mantissas of amax/7's binade).
+    amax = w.view(3, 8, 2, 128).abs().amax(dim=-1)
+    for a_, s_ in zip(amax.flatten().tolist(), s.float().flatten().tolist()):
+        t = a_ / 7.0
+        e = math.floor(math.log2(t))
+        cands = [(16 + i) / 16.0 * 2.0 ** e for i in range(17)]
+        assert s_ == min(c for c in cands if c >= t)
+    # Symmetric rounding: q = round(w / s), |q| <= 7.
     sf = s.float().repeat_interleave(128, dim=-1)
-    assert torch.equal(q.float(), torch.round(w / sf).clamp(-8, 7))
+    assert torch.equal(q.float(), torch.round(w / sf))
+    assert q.abs().max() <= 7
     dq = O.dequant_int4_group(packed, s)
-    # Rounding to the grid (s/2) plus the bf16 rounding of q*s (half an ulp).
-    assert ((dq.float() - w).abs() <= sf / 2 + dq.float().abs() * 2 ** -8 + 1e-12).all()
+    # q*s is exact in bf16 (so kernels may scale after the dot product) ...
+    assert torch.equal(dq.double(), q.double() * sf.double())
+    # ... and within half a step of w.
+    assert ((dq.float() - w).abs() <= sf / 2 + 1e-12).all()
 
 
 def test_quantised_moe_oracle_vs_textbook():
