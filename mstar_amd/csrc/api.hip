@@ -57,10 +57,14 @@ struct Plan {
   // The routing launch also quantises the hidden rows (hq/hs in the
   // workspace) for the streaming gate_up GEMM.
   bool route_quant = false;
+  // 256-row FP8 GEMMs: the intermediates (FP8 activation codes and, when
+  // reduced, the down output) are stored by sorted position, so every tile
+  // reads and writes contiguous rows; the top-k sum gathers through pos_of.
+  bool by_pos = false;
   int bm = 16;
   int64_t slots = 0, max_padded = 0, max_blocks = 0;
   size_t off_sorted, off_eids, off_ntpp, off_eoff, off_ecnt, off_c2, off_c3, off_hq, off_hs,
-      off_cq, off_cs, off_scratch, scratch_bytes, off_tw, off_ids, total;
+      off_cq, off_cs, off_scratch, scratch_bytes, off_tw, off_ids, off_pos, total;
 };
 
 // with_route: the plan also holds the router outputs and the routing scratch
@@ -103,9 +107,12 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->off_ntpp = take(4);
   pl->off_eoff = take((size_t)(E + 1) * 4);
   pl->off_ecnt = take((size_t)E * 4);
-  pl->off_c2 = take((size_t)pl->slots * I * 2);
-  pl->off_c3 = reduce ? take((size_t)pl->slots * H * 2) : 0;
   const bool fp8_tiled = quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream;
+  pl->by_pos = fp8_tiled && pl->bm == kBigBlockM;
+  // Rows of the position-indexed buffers: every position of every block.
+  const size_t pos_rows = (size_t)pl->max_blocks * pl->bm;
+  pl->off_c2 = pl->by_pos ? 0 : take((size_t)pl->slots * I * 2);
+  pl->off_c3 = reduce ? take((pl->by_pos ? pos_rows : (size_t)pl->slots) * H * 2) : 0;
   // With the router in the plan, the routing launch quantises the hidden
   // rows: widened to bf16 for the router-ids streaming kernel, as e4m3fn
   // codes for the tiled FP8 GEMM (multi-workgroup routing only).
@@ -114,8 +121,10 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
                                     route_is_grid(M, top_k)));
   pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;
   pl->off_hs = fp8_tiled || pl->route_quant ? take((size_t)M * (H / 128) * 4) : 0;
-  pl->off_cq = fp8_tiled ? take((size_t)pl->slots * I) : 0;
-  pl->off_cs = fp8_tiled ? take((size_t)pl->slots * (I / 128) * 4) : 0;
+  const size_t cq_rows = pl->by_pos ? pos_rows : (size_t)pl->slots;
+  pl->off_cq = fp8_tiled ? take(cq_rows * I) : 0;
+  pl->off_cs = fp8_tiled ? take(cq_rows * (I / 128) * 4) : 0;
+  pl->off_pos = pl->by_pos ? take((size_t)pl->slots * 4) : 0;
   pl->scratch_bytes = with_route ? route_scratch_bytes(M, top_k, E) : align_scratch_bytes(pl->slots, E);
   pl->off_scratch = take(pl->scratch_bytes);
   pl->off_tw = with_route ? take((size_t)pl->slots * 4) : 0;
@@ -153,7 +162,7 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
   int32_t* ntpp = (int32_t*)(ws + pl.off_ntpp);
   int32_t* eoff = (int32_t*)(ws + pl.off_eoff);
   int32_t* ecnt = (int32_t*)(ws + pl.off_ecnt);
-  void* cache2 = ws + pl.off_c2;
+  void* cache2 = pl.by_pos ? nullptr : (void*)(ws + pl.off_c2);
   void* cache3 = reduce_results ? (void*)(ws + pl.off_c3) : out;
   const int bkind = quant == MSTAR_QUANT_FP8_W8A8 ? B_FP8BLK : quant == MSTAR_QUANT_W4A16 ? B_INT4G : B_H16;
   GemmArgs g1 = {};
@@ -213,6 +222,12 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
     // the smaller tiles store bf16 and a quantisation launch follows.
     const bool fused_q = pl.bm == kBigBlockM;
     if (fused_q) { g1.cq = cq; g1.cs = cs; }
+    if (pl.by_pos) {
+      g1.pos_out = 1;
+      g1.pos_of = (int32_t*)(ws + pl.off_pos);
+      g2.pos_in = 1;
+      g2.pos_out = reduce_results;
+    }
     st = launch_tile_gemm(g1, A_FP8G, B_FP8BLK, EPI_ACT, act_dtype, true, pl.bm, stream);
     if (st != kOk) return st;
     if (!fused_q) {
@@ -229,6 +244,9 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
     st = launch_tile_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, true, pl.bm, stream);
     if (st != kOk) return st;
   }
+  if (reduce_results && pl.by_pos)
+    return launch_sum_reduce_pos(cache3, (const int32_t*)(ws + pl.off_pos), out, act_dtype, M, top_k, H,
+                                 stream);
   if (reduce_results)
     return launch_sum_reduce(cache3, out, act_dtype, M, top_k, H, 1.0f, stream);
   return kOk;

@@ -33,8 +33,11 @@ __global__ __launch_bounds__(256) void act_and_mul_kernel(const uint16_t* __rest
   *(v4i*)(out + r * inter + c) = o;
 }
 
-template <int DT>
+// POS: row j of token t is in[pos_of[t * topk + j]] (rows by sorted
+// position) instead of in[t * topk + j].
+template <int DT, bool POS>
 __global__ __launch_bounds__(256) void sum_reduce_kernel(const uint16_t* __restrict__ in,
+                                                         const int32_t* __restrict__ pos_of,
                                                          uint16_t* __restrict__ out,
                                                          int64_t tokens, int topk,
                                                          int64_t hidden, float scale) {
@@ -43,14 +46,29 @@ __global__ __launch_bounds__(256) void sum_reduce_kernel(const uint16_t* __restr
   if (v >= tokens * vecs) return;
   const int64_t t = v / vecs, c = (v % vecs) * 8;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  const uint16_t* base = in + t * topk * hidden + c;
-  for (int j = 0; j < topk; ++j) {
-    v4i x = *(const v4i*)(base + (int64_t)j * hidden);
+  auto add = [&](const v4i& x) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       acc[2 * i] += h16_to_f32<DT>((uint32_t)x[i] & 0xffff);
       acc[2 * i + 1] += h16_to_f32<DT>((uint32_t)x[i] >> 16);
     }
+  };
+  // Eight rows at a time: their loads (and, by position, the position loads
+  // before them) are all in flight together; the sum stays in row order.
+  int j = 0;
+  for (; j + 8 <= topk; j += 8) {
+    int64_t row[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) row[u] = POS ? (int64_t)pos_of[t * topk + j + u] : t * topk + j + u;
+    v4i x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = *(const v4i*)(in + row[u] * hidden + c);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) add(x[u]);
+  }
+  for (; j < topk; ++j) {
+    const int64_t row = POS ? (int64_t)pos_of[t * topk + j] : t * topk + j;
+    add(*(const v4i*)(in + row * hidden + c));
   }
   v4i o;
 #pragma unroll
@@ -92,11 +110,33 @@ int launch_sum_reduce(const void* in, void* out, int dtype, int64_t tokens, int6
   if (tokens == 0) return kOk;
   dim3 grid((unsigned)((tokens * (hidden / 8) + 255) / 256));
   if (dtype == kBF16)
-    sum_reduce_kernel<kBF16><<<grid, 256, 0, stream>>>((const uint16_t*)in, (uint16_t*)out, tokens,
+    sum_reduce_kernel<kBF16, false><<<grid, 256, 0, stream>>>((const uint16_t*)in, nullptr, (uint16_t*)out, tokens,
                                                        (int)topk, hidden, scale);
   else if (dtype == kF16)
-    sum_reduce_kernel<kF16><<<grid, 256, 0, stream>>>((const uint16_t*)in, (uint16_t*)out, tokens,
+    sum_reduce_kernel<kF16, false><<<grid, 256, 0, stream>>>((const uint16_t*)in, nullptr, (uint16_t*)out, tokens,
                                                       (int)topk, hidden, scale);
+  else {
+    set_last_error("moe_sum_reduce: dtype must be bf16 or fp16");
+    return kUnsupported;
+  }
+  return launch_status("moe_sum_reduce");
+}
+
+int launch_sum_reduce_pos(const void* in, const int32_t* pos_of, void* out, int dtype,
+                          int64_t tokens, int64_t topk, int64_t hidden, hipStream_t stream) {
+  if (tokens < 0 || topk <= 0 || hidden <= 0 || hidden % 8 != 0 || (tokens > 0 && !pos_of)) {
+    set_last_error("moe_sum_reduce: hidden must be a positive multiple of 8 (hidden=%lld)",
+                   (long long)hidden);
+    return kInvalidArgument;
+  }
+  if (tokens == 0) return kOk;
+  dim3 grid((unsigned)((tokens * (hidden / 8) + 255) / 256));
+  if (dtype == kBF16)
+    sum_reduce_kernel<kBF16, true><<<grid, 256, 0, stream>>>((const uint16_t*)in, pos_of, (uint16_t*)out,
+                                                             tokens, (int)topk, hidden, 1.0f);
+  else if (dtype == kF16)
+    sum_reduce_kernel<kF16, true><<<grid, 256, 0, stream>>>((const uint16_t*)in, pos_of, (uint16_t*)out,
+                                                            tokens, (int)topk, hidden, 1.0f);
   else {
     set_last_error("moe_sum_reduce: dtype must be bf16 or fp16");
     return kUnsupported;

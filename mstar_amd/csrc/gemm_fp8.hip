@@ -160,8 +160,9 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     };
 #pragma unroll
     for (int q = 0; q < AI; ++q) {
-      const int s = slot_of(t, buf, wave * (BM / 8) + q * 8 + (lane >> 3));
-      const int ar = s >= 0 ? s / p.top_k : 0;
+      const int rr = wave * (BM / 8) + q * 8 + (lane >> 3);
+      const int s = slot_of(t, buf, rr);
+      const int ar = p.pos_in ? mb * BM + rr : s >= 0 ? s / p.top_k : 0;
       a_off[q] = (uint32_t)((int64_t)ar * p.lda) + lchunk;
     }
 #pragma unroll
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     if constexpr (BLOCKSCALE) {
       if (wave < 4) {
         const int s = slot_of(t, buf, wave * 64 + lane);
-        sc_src = p.a_scale + (int64_t)(s >= 0 ? s / p.top_k : 0) * p.ld_as;
+        sc_src = p.a_scale + (int64_t)(p.pos_in ? mb * BM + wave * 64 + lane : s >= 0 ? s / p.top_k : 0) * p.ld_as;
       } else if (wave == 4) {
         const int ww = (lane / NB) % WN, j = lane % NB;
         const int r = brow_of(ww * WTN + j * 32);
@@ -275,9 +276,12 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   for (int n = 0; n < kParts; ++n) issue_part(n, ik, ist);
 
   // Output buffers (sizes below 4 GiB: checked on the host).
-  const auto rs_c = make_rsrc(p.C, (uint32_t)((int64_t)p.M * p.ldc * 2));
-  const auto rs_cq = make_rsrc(p.cq, (uint32_t)((int64_t)p.M * p.inter));
-  const auto rs_cs = make_rsrc(p.cs, (uint32_t)((int64_t)p.M * (p.inter / 128) * 4));
+  // Rows by position reach past the slot count: up to the padded total.
+  const int64_t out_rows = p.pos_out ? (int64_t)p.m_blocks * BM : p.M;
+  const auto rs_c = make_rsrc(p.C, (uint32_t)(out_rows * p.ldc * 2));
+  const auto rs_cq = make_rsrc(p.cq, (uint32_t)(out_rows * p.inter));
+  const auto rs_cs = make_rsrc(p.cs, (uint32_t)(out_rows * (p.inter / 128) * 4));
+  const auto rs_pos = make_rsrc(p.pos_of, (uint32_t)(p.M * 4));
   // Stores each wave issues in a tile's epilogue (0: a path with a variable
   // count, waited for in full).
   int epi_stores;
@@ -386,6 +390,17 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     int lane_e;
     asm volatile("v_mov_b32 %0, %1" : "=v"(lane_e) : "v"(lane));
     const int l32 = lane_e & 31, lh = lane_e >> 5;
+    // Output row of tile row `row` holding `slot` (-1: padding, not written).
+    auto orow = [&](int row, int slot) -> int {
+      return slot < 0 ? -1 : p.pos_out ? mb * BM + row : slot;
+    };
+    if (GROUPED && p.pos_of && nt == 0 && wave < 4) {
+      // Position of each slot of the m-block (one buffer store per wave:
+      // extra stores only make the next tile's first wait stricter).
+      const int row = wave * 64 + lane_e, slot = slot_of(t, buf, row);
+      const uint32_t off = slot >= 0 ? (uint32_t)slot * 4u : kOffNone;
+      __builtin_amdgcn_raw_buffer_store_b32(mb * BM + row, rs_pos, off, 0, 0);
+    }
     // The staged paths store through buffer resources: a lane with nothing
     // to write stores out of range (dropped), so every wave issues a fixed
     // number of stores per tile -- the next tile's first wait counts them.
@@ -450,9 +465,9 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
                 cvt_fp8x4(y[0], y[1], y[2], y[3]);
           }
           {  // one lane per token writes the scale; the others' stores fall outside the buffer
-            const int slot = slot_of(t, buf, row);
-            const uint32_t off = slot >= 0 && wn == 0 && lh == 0
-                                     ? (uint32_t)(((int64_t)slot * (p.inter / 128) + nt) * 4) : kOffNone;
+            const int orw = orow(row, slot_of(t, buf, row));
+            const uint32_t off = orw >= 0 && wn == 0 && lh == 0
+                                     ? (uint32_t)(((int64_t)orw * (p.inter / 128) + nt) * 4) : kOffNone;
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, sc), rs_cs, off, 0, 0);
           }
         }
@@ -461,8 +476,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
         for (int pass = 0; pass < BM / 8 / 8; ++pass) {  // 8 rows per wave instruction
           const int row = wave * (BM / 8) + pass * 8 + (lane_e >> 3), u = lane_e & 7;
           const v4i val = *(const v4i*)(stg + row * 128 + ((u ^ (row & 7)) << 4));
-          const int slot = slot_of(t, buf, row);
-          const uint32_t off = slot >= 0 ? (uint32_t)((int64_t)slot * p.inter + nt * (BN / 2) + u * 16) : kOffNone;
+          const int orw = orow(row, slot_of(t, buf, row));
+          const uint32_t off = orw >= 0 ? (uint32_t)((int64_t)orw * p.inter + nt * (BN / 2) + u * 16) : kOffNone;
           __builtin_amdgcn_raw_buffer_store_b128(val, rs_cq, off, 0, 0);
         }
       } else if ((p.ldc & 7) == 0 && (p.inter & 7) == 0) {
@@ -487,17 +502,17 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
         for (int pass = 0; pass < BM / 8 / 4; ++pass) {  // 4 rows per wave instruction
           const int row = wave * (BM / 8) + pass * 4 + (lane_e >> 4), u = lane_e & 15;
           const v4i val = *(const v4i*)(stg + row * 256 + ((u ^ (row & 15)) << 4));
-          const int slot = slot_of(t, buf, row);
+          const int orw = orow(row, slot_of(t, buf, row));
           const int gcol = nt * (BN / 2) + u * 8;
-          const uint32_t off = slot >= 0 && gcol < p.inter ? (uint32_t)(((int64_t)slot * p.ldc + gcol) * 2) : kOffNone;
+          const uint32_t off = orw >= 0 && gcol < p.inter ? (uint32_t)(((int64_t)orw * p.ldc + gcol) * 2) : kOffNone;
           __builtin_amdgcn_raw_buffer_store_b128(val, rs_c, off, 0, 0);
         }
       } else {
 #pragma unroll
         for (int i = 0; i < MB; ++i) {
-          const int slot = slot_of(t, buf, wm * WTM + i * 32 + l32);
-          if (slot < 0) continue;
-          uint16_t* crow = C + (int64_t)slot * p.ldc;
+          const int orw = orow(wm * WTM + i * 32 + l32, slot_of(t, buf, wm * WTM + i * 32 + l32));
+          if (orw < 0) continue;
+          uint16_t* crow = C + (int64_t)orw * p.ldc;
 #pragma unroll
           for (int jq = 0; jq < NB / 2 * 4; ++jq) {
             const int jj = jq / 4, q = jq % 4;
@@ -546,9 +561,9 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
           for (int pass = 0; pass < 8; ++pass) {  // 2 rows per wave instruction
             const int lr2 = wave * 16 + pass * 2 + (lane_e >> 5), u = lane_e & 31;
             const v4i val = *(const v4i*)(stg + lr2 * 512 + ((u ^ (lr2 & 31)) << 4));
-            const int slot = slot_of(t, buf, (lr2 >> 5) * WTM + i * 32 + (lr2 & 31));
+            const int orw = orow((lr2 >> 5) * WTM + i * 32 + (lr2 & 31), slot_of(t, buf, (lr2 >> 5) * WTM + i * 32 + (lr2 & 31)));
             const int col = nt * BN + u * 8;
-            const uint32_t off = slot >= 0 && col < p.N ? (uint32_t)(((int64_t)slot * p.ldc + col) * 2) : kOffNone;
+            const uint32_t off = orw >= 0 && col < p.N ? (uint32_t)(((int64_t)orw * p.ldc + col) * 2) : kOffNone;
             __builtin_amdgcn_raw_buffer_store_b128(val, rs_c, off, 0, 0);
           }
           if (i + 1 < MB) lds_barrier();  // half i is read before half i + 1 lands
@@ -559,7 +574,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
           const int row = wm * WTM + i * 32 + l32;
           const int slot = slot_of(t, buf, row);
           if (slot < 0) continue;
-          uint16_t* crow = C + (int64_t)slot * p.ldc;
+          uint16_t* crow = C + (int64_t)orow(row, slot) * p.ldc;
           const float rs = row_factor(row, slot);
 #pragma unroll
           for (int jq = 0; jq < NB * 4; ++jq) {
@@ -602,7 +617,12 @@ static int run_big(const GemmArgs& a, hipStream_t stream) {
 }
 
 int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t stream) {
-  if (a.M * a.ldc * 2 >= (int64_t)kOffNone || a.M * a.inter >= (int64_t)kOffNone) {
+  if ((a.pos_out || a.pos_in || a.pos_of) && !grouped) {
+    set_last_error("gemm_fp8_big: position-indexed rows need grouped mode");
+    return kInvalidArgument;
+  }
+  const int64_t out_rows = a.pos_out ? (int64_t)a.m_blocks * kBigBM : a.M;
+  if (out_rows * a.ldc * 2 >= (int64_t)kOffNone || out_rows * a.inter >= (int64_t)kOffNone) {
     set_last_error("gemm_fp8_big: output larger than 4 GiB");
     return kUnsupported;
   }
@@ -615,7 +635,8 @@ int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t st
     return kInvalidArgument;
   }
   // Row offsets are 32-bit byte offsets.
-  const int64_t a_rows = grouped ? (a.M + a.top_k - 1) / (a.top_k > 0 ? a.top_k : 1) : a.M;
+  const int64_t a_rows = a.pos_in ? (int64_t)a.m_blocks * kBigBM
+                       : grouped ? (a.M + a.top_k - 1) / (a.top_k > 0 ? a.top_k : 1) : a.M;
   if (a_rows * a.lda >= ((int64_t)1 << 32) || (int64_t)a.N * a.ldb >= ((int64_t)1 << 32)) {
     set_last_error("gemm_fp8_big: operand larger than 4 GiB");
     return kUnsupported;

@@ -55,6 +55,10 @@ int launch_act_and_mul(const void* gate_up, void* out, int dtype, int64_t rows, 
                        int activation, hipStream_t stream);
 int launch_sum_reduce(const void* in, void* out, int dtype, int64_t tokens, int64_t topk,
                       int64_t hidden, float scale, hipStream_t stream);
+// The same sum over rows stored by sorted position: row j of token t is
+// in[pos_of[t * topk + j]].
+int launch_sum_reduce_pos(const void* in, const int32_t* pos_of, void* out, int dtype,
+                          int64_t tokens, int64_t topk, int64_t hidden, hipStream_t stream);
 
 // moe_gemm.hip --------------------------------------------------------------
 // Operand encodings.
@@ -107,6 +111,14 @@ struct GemmArgs {
   // A_FP8G rows hold the e4m3fn values widened to bf16 (2 bytes per
   // element, lda in elements) instead of e4m3fn bytes.
   int a_q16;
+  // Grouped 256-row FP8 kernel only: intermediates indexed by sorted
+  // position (m-block * 256 + row of the block in sorted_ids) instead of by
+  // slot, so that a tile's rows are contiguous.  pos_out: C / cq / cs rows
+  // are positions (padding rows are not written); pos_in: A and a_scale rows
+  // are positions.  pos_of: when set, the tiles of n-tile 0 record
+  // pos_of[slot] = position.
+  int pos_out, pos_in;
+  int32_t* pos_of;
 };
 
 // Tiled grouped / dense GEMM (LDS-staged MFMA tiles); bm is the row block.

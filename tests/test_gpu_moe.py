@@ -160,6 +160,25 @@ def test_fused_experts_fp8_thinker(M, bias):
     assert_moe_close(out, ref, what=f"fp8 M={M}")
 
 
+@pytest.mark.parametrize("reduce", [True, False])
+def test_fused_experts_fp8_position_rows(reduce):
+    """4096 tokens x top-8 over 128 experts: the 256-row FP8 kernel stores the
+    intermediates by sorted position; with reduce_results=False the down GEMM
+    writes per slot ([tokens, top_k, hidden]) from position-indexed inputs."""
+    from mstar_amd.fused_moe import fused_experts
+    H, E, I, k, M = 2048, 128, 768, 8, 4096
+    q1, s1, q2, s2 = _fp8_weights(H, E, I)
+    x = _hidden(M, H, seed=41)
+    tw, ti = _routing(M, E, k, seed=41, bias=True)
+    out = fused_experts(x.to(DEV), q1, q2, tw.to(DEV), ti.to(DEV), quant="fp8_w8a8",
+                        w1_scale=s1, w2_scale=s2, block_shape=(128, 128), reduce_results=reduce)
+    q1c, s1c, q2c, s2c = q1.cpu(), s1.cpu(), q2.cpu(), s2.cpu()
+    ref = O.fused_experts_rounding(x, None, None, tw, ti, reduce_results=reduce,
+                                   w1_dq=lambda e: O.dequant_fp8_block(q1c[e], s1c[e]),
+                                   w2_dq=lambda e: O.dequant_fp8_block(q2c[e], s2c[e]), act_quant=True)
+    assert_moe_close(out, ref, what=f"fp8 position rows reduce={reduce}")
+
+
 def test_fused_experts_fp8_bm128_path():
     from mstar_amd.fused_moe import fused_experts
     H, E, I, k, M = 256, 8, 256, 2, 1024
