@@ -253,13 +253,28 @@ __device__ __forceinline__ v8s int4x8_dequant_bf16(uint32_t w, float s, float m8
 }
 
 // Eight int4 codes (element j in bits 4j of w) as bf16 128 + u, two per
-// dword in the order 0, 4, 1, 5, 2, 6, 3, 7: 128 + u is bf16 0x4300 | u, so
-// each pair is one shift and one and-or.  A dot product over these values
-// is sum (u + 128) x; sum (u - 8) x follows by subtracting 136 sum x.
-__device__ __forceinline__ v8s int4x8_bias128(uint32_t w) {
+// dword in the order 0, 4, 1, 5, 2, 6, 3, 7: 128 + u is bf16 0x4300 | u.  A
+// dot product over these values is sum (u + 128) x; sum (u - 8) x follows
+// by subtracting 136 sum x.  Each pair is one v_bfi_b32 (mask m =
+// 0x000f000f in an SGPR, bias c = 0x43004300 in a VGPR: both from
+// int4_bias_consts) after a shift.
+struct Int4BiasConsts {
+  uint32_t m, c;
+};
+__device__ __forceinline__ Int4BiasConsts int4_bias_consts() {
+  Int4BiasConsts k;
+  asm volatile("s_mov_b32 %0, 0x000f000f" : "=s"(k.m));
+  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(k.c));
+  return k;
+}
+__device__ __forceinline__ v8s int4x8_bias128(uint32_t w, Int4BiasConsts k) {
   v4i r;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) r[j] = (int)(((w >> (4 * j)) & 0x000F000Fu) | 0x43004300u);
+  for (int j = 0; j < 4; ++j) {
+    uint32_t y;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(y) : "s"(k.m), "v"(w >> (4 * j)), "v"(k.c));
+    r[j] = (int)y;
+  }
   return __builtin_bit_cast(v8s, r);
 }
 

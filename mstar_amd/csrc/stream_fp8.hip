@@ -371,7 +371,11 @@ __global__ __launch_bounds__(256) void stream_fp8_kernel(GemmArgs p) {
 // with each 128-element block's sum.
 enum : int { STAGE_Q16 = 0, STAGE_H16 = 1, STAGE_W4 = 2 };
 constexpr int kCuThreads = 512;
-constexpr int kCuWaves = kCuThreads / 64;
+// int4 weights: sixteen waves per CU (their rings are half the size), so
+// that more waves' dependent LDS / VALU / MFMA chains overlap.
+constexpr int kCuThreadsW4 = 1024;
+template <bool W4>
+__host__ __device__ constexpr int cu_waves() { return (W4 ? kCuThreadsW4 : kCuThreads) / 64; }
 constexpr int kCuRing = 3;        // ring slots per wave
 constexpr size_t kCuLdsMax = 160 * 1024;
 constexpr int kDmaAux = 2;        // cache policy of the weight stream (streaming)
@@ -380,22 +384,28 @@ template <int KS>
 __host__ __device__ constexpr int cu_kc() { return KS % 2 == 0 ? 2 : KS; }  // K-steps per chunk
 template <int KS>
 __host__ __device__ constexpr int cu_pitch() { return KS * 256 + 16; }     // bytes per staged bf16 row
+// int4 weights: K-steps per chunk (a 128-byte line of a row holds two), and
+// the ring slot: KC / 2 lines of 16 rows, then the rows' KC bf16 scales.
 template <int KS>
+__host__ __device__ constexpr int cu_w4_kc() { return 2; }
+template <int KS>
+__host__ __device__ constexpr int cu_w4_slot() { return cu_w4_kc<KS>() * (1024 + 32); }
+template <int KS, bool W4 = false>
 __host__ __device__ constexpr size_t cu_ring_bytes() {
-  return (size_t)kCuWaves * kCuRing * cu_kc<KS>() * 2048;
+  return (size_t)cu_waves<W4>() * kCuRing * (W4 ? cu_w4_slot<KS>() : cu_kc<KS>() * 2048);
 }
 // LDS layout: rings | sAct[E] sCnt[E] sOff[E] sList[M'] | sSc[cap][KS] sRw[cap] |
 // rows[cap][pitch]
 __host__ __device__ inline size_t cu_lists_bytes(int E, int64_t M) {
   return ((size_t)3 * E + (size_t)((M + 3) & ~3ll)) * 4;
 }
-template <int KS>
+template <int KS, bool W4 = false>
 __host__ __device__ inline size_t cu_sc_off(int E, int64_t M) {
-  return cu_ring_bytes<KS>() + cu_lists_bytes(E, M);
+  return cu_ring_bytes<KS, W4>() + cu_lists_bytes(E, M);
 }
-template <int KS>
+template <int KS, bool W4 = false>
 __host__ __device__ inline size_t cu_rows_off(int E, int64_t M, int cap) {
-  return (cu_sc_off<KS>(E, M) + (size_t)cap * (KS + 1) * 4 + 15) & ~(size_t)15;
+  return (cu_sc_off<KS, W4>(E, M) + (size_t)cap * (KS + 1) * 4 + 15) & ~(size_t)15;
 }
 
 // Wait for the oldest of `ahead` chunks in flight (DPC DMA instructions
@@ -415,33 +425,42 @@ __device__ __forceinline__ void wait_leaving_chunks(int ahead) {
   }
 }
 
+// Swizzle of the 16-byte pieces of int4 ring row r (rows 128 bytes apart):
+// the 16 rows' reads of one logical piece fall in distinct banks.
+__device__ __forceinline__ int w4_swz(int r) { return (r >> 1) & 7; }
+
 template <int EPI, int KS, int STAGE>
-__global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, int cap) {
+__global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void stream_fp8_cu_kernel(
+    GemmArgs p, int cap) {
   constexpr bool W4 = STAGE == STAGE_W4;
   static_assert(!W4 || KS % 2 == 0, "int4 chunks are two K-steps");
   constexpr int PITCH = cu_pitch<KS>();
-  constexpr int KC = W4 ? 2 : cu_kc<KS>();  // K-steps per chunk
+  constexpr int KC = W4 ? cu_w4_kc<KS>() : cu_kc<KS>();  // K-steps per chunk
   constexpr int CH = KS / KC;               // chunks per item
-  constexpr int WAVE_RING = kCuRing * cu_kc<KS>() * 2048;  // ring bytes per wave
-  // Ring slot: FP8 -- 16 rows x KC x 128 bytes; int4 -- 16 rows x KC x 64
-  // bytes, then the 16 rows' KC bf16 scales (4 bytes a row).
-  constexpr int SLOT = W4 ? KC * 1024 + 128 : KC * 2048;
+  // Ring slot: FP8 -- 16 rows x KC x 128 bytes; int4 -- KC / 2 lines (two
+  // K-steps each) of the 16 rows as blocks of 8 rows x 128 bytes (pieces
+  // swizzled), then the 16 rows' KC bf16 scales (2 KC bytes a row).
+  constexpr int SLOT = W4 ? cu_w4_slot<KS>() : KC * 2048;
+  constexpr int WAVE_RING = W4 ? kCuRing * SLOT : kCuRing * cu_kc<KS>() * 2048;  // ring bytes per wave
   constexpr int RING = WAVE_RING / SLOT;    // slots per wave
   constexpr int DPC = W4 ? KC + 1 : 2 * KC;  // DMA instructions per chunk
+  constexpr int W4_PR = KC / 2;             // int4: 4-byte scale pieces per row
   static_assert(RING >= 3 && RING <= 6, "ring depth");
-  constexpr int SPT = (int)(kStreamMaxIdsSlots / kCuThreads);  // router ids per thread
+  constexpr int NTH = W4 ? kCuThreadsW4 : kCuThreads;  // threads of the workgroup
+  constexpr int NWV = NTH / 64;                          // its waves
+  constexpr int SPT = (int)(kStreamMaxIdsSlots / NTH);  // router ids per thread
   // Waves that stage activation rows; the others prefetch weights meanwhile.
   constexpr int SW = STAGE == STAGE_Q16 ? 2 : 4;
   typedef __attribute__((address_space(3))) void* lds_void_ptr;
   extern __shared__ __align__(16) uint8_t smem[];
   const int E = p.num_experts;
-  int* sAct = (int*)(smem + cu_ring_bytes<KS>());
+  int* sAct = (int*)(smem + cu_ring_bytes<KS, W4>());
   int* sCnt = sAct + E;
   int* sOff = sCnt + E;
   int* sList = sOff + E;
-  float* sSc = (float*)(smem + cu_sc_off<KS>(E, p.M));
+  float* sSc = (float*)(smem + cu_sc_off<KS, W4>(E, p.M));
   float* sRw = sSc + cap * KS;  // routed weight of each staged row
-  uint8_t* sRows = smem + cu_rows_off<KS>(E, p.M, cap);
+  uint8_t* sRows = smem + cu_rows_off<KS, W4>(E, p.M, cap);
   __shared__ uint32_t sMask[32];  // active experts (E <= 1024)
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -452,13 +471,13 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   uint8_t* ring = smem + w * WAVE_RING;
 
   // ---- prologue 1: per-expert counts and the active-expert mask.
-  for (int e = tid; e < E; e += kCuThreads) sCnt[e] = 0;
+  for (int e = tid; e < E; e += NTH) sCnt[e] = 0;
   if (tid < 32) sMask[tid] = 0;
   lds_sync();
   int my_e[SPT], my_pos[SPT];
 #pragma unroll
   for (int j = 0; j < SPT; ++j) {
-    const int i = tid + j * kCuThreads;
+    const int i = tid + j * NTH;
     int e = -1;
     if (i < p.M) {
       const int64_t v = p.ids_dtype == kI64 ? ((const int64_t*)p.topk_ids)[i]
@@ -495,19 +514,29 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   // rows r8 and 8 + r8 of the item, physical chunk pc = logical pc ^ r8.
   const int r8 = lane >> 3;
   const uint32_t lc16 = (uint32_t)(((lane & 7) ^ r8) * 16);
+  // int4 rows (see dma_rows): the source piece of lane l in instructions 0
+  // and 1, and the byte distance from row r8 to row 8 + r8.
+  const uint32_t w4_lc0 = (uint32_t)(((lane & 7) ^ w4_swz(r8)) * 16);
+  const uint32_t w4_lc1 = (uint32_t)(((lane & 7) ^ w4_swz(8 + r8)) * 16);
+  const int64_t w4_q1 = (int64_t)(EPI == EPI_ACT ? p.inter : 8) * p.ldb * 4;
+  const Int4BiasConsts w4k = int4_bias_consts();
   auto dma_rows = [&](int e, int g, const uint8_t*& s0, const uint8_t*& s1) {
     if constexpr (W4) {
-      // Lane l: item row l / 4, 16-byte piece l % 4 of a K-step's 64 bytes;
-      // lanes 0-15 also fetch item row l's scales.  Item rows 0-7 are gate
-      // rows and 8-15 the matching up rows (EPI_ACT).
+      // A chunk's two K-steps are one 128-byte line of each row.  DMA
+      // instruction q moves item rows 8q .. 8q+7: lane l row 8q + l / 8,
+      // physical piece l % 8 holding logical piece (l % 8) ^ w4_swz(row)
+      // (logical piece = 4 * K-step + 16-byte piece of the step's 64 bytes).
+      // s0 is row r8 of instruction 0; instruction 1's row is w4_q1 bytes
+      // further.  Lanes 0-15 also fetch item row l's scales (s1).  Item rows
+      // 0-7 are gate rows and 8-15 the matching up rows (EPI_ACT).
       auto row_of = [&](int rr) -> int {
         if constexpr (EPI == EPI_ACT) return rr < 8 ? g * 8 + rr : p.inter + g * 8 + rr - 8;
         else return g * 16 + rr;
       };
       const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride * 4;  // int32 words
-      s0 = Be + (int64_t)row_of(lane >> 2) * p.ldb * 4 + (lane & 3) * 16;
+      s0 = Be + (int64_t)row_of(r8) * p.ldb * 4;
       s1 = (const uint8_t*)((const uint16_t*)p.b_scale + (int64_t)e * p.bs_estride +
-                            (int64_t)row_of(lane & 15) * p.bs_ld);
+                            (int64_t)row_of((lane / W4_PR) & 15) * p.bs_ld) + (lane % W4_PR) * 4;
       return;
     }
     const uint8_t* Be = (const uint8_t*)p.B + (int64_t)e * p.b_estride;
@@ -526,10 +555,14 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
     uint8_t* dst = ring + slot * SLOT;
     if constexpr (W4) {
 #pragma unroll
-      for (int kk = 0; kk < KC; ++kk)
-        __builtin_amdgcn_global_load_lds((const void*)(s0 + (c * KC + kk) * 64),
-                                         (lds_void_ptr)(dst + kk * 1024), 16, 0, kDmaAux);
-      if (lane < 16)  // row lane's scales of K-steps c*KC, c*KC + 1
+      for (int h = 0; h < KC / 2; ++h) {  // line h of the chunk: rows 0-7, then 8-15
+        const int64_t lo = (int64_t)(c * (KC / 2) + h) * 128;
+        __builtin_amdgcn_global_load_lds((const void*)(s0 + lo + w4_lc0), (lds_void_ptr)(dst + 2 * h * 1024),
+                                         16, 0, kDmaAux);
+        __builtin_amdgcn_global_load_lds((const void*)(s0 + w4_q1 + lo + w4_lc1),
+                                         (lds_void_ptr)(dst + (2 * h + 1) * 1024), 16, 0, kDmaAux);
+      }
+      if (lane < 16 * W4_PR)  // piece lane % W4_PR of row lane / W4_PR's scales of the chunk
         __builtin_amdgcn_global_load_lds((const void*)(s1 + c * KC * 2), (lds_void_ptr)(dst + KC * 1024),
                                          4, 0, 0);
       return;
@@ -578,7 +611,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
   lds_sync();
 #pragma unroll
   for (int j = 0; j < SPT; ++j)
-    if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * kCuThreads;
+    if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * NTH;
   lds_sync();
   const int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
 
@@ -704,7 +737,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
     return rb < re;
   };
   auto first_unit = [&](int it, Cur& cu) -> bool {  // first unit at or after item `it`
-    for (; it < i1; it += kCuWaves) {
+    for (; it < i1; it += NWV) {
       int rb, re;
       if (item_rows(it, rb, re)) {
         cu = Cur{it, rb, 0};
@@ -722,7 +755,7 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
       cu.c = 0;
       return true;
     }
-    return first_unit(cu.it + kCuWaves, cu);
+    return first_unit(cu.it + NWV, cu);
   };
 
   bool use_prefetch = prefetched;
@@ -816,24 +849,29 @@ __global__ __launch_bounds__(kCuThreads) void stream_fp8_cu_kernel(GemmArgs p, i
         const int c = __builtin_amdgcn_readfirstlane(cc.c);
         if constexpr (W4) {
           // Scales of rows 4 lg .. +3 (the rows this lane's results belong
-          // to) for both K-steps: 16 contiguous bytes.
-          const v4i sc4 = *(const v4i*)(wslot + KC * 1024 + lg * 16);
+          // to) for the chunk's K-steps: 8 KC contiguous bytes.
+          v4i sc4[W4_PR];
+#pragma unroll
+          for (int h = 0; h < W4_PR; ++h) sc4[h] = *(const v4i*)(wslot + KC * 1024 + lg * 8 * KC + h * 16);
 #pragma unroll
           for (int kk = 0; kk < KC; ++kk) {
             const int ks = c * KC + kk;
-            const v4i wq = *(const v4i*)(wslot + kk * 1024 + l16 * 64 + lg * 16);
+            const v4i wq = *(const v4i*)(wslot + ((kk >> 1) * 2 + (l16 >> 3)) * 1024 + (l16 & 7) * 128 +
+                                         ((((kk & 1) * 4 + lg) ^ w4_swz(l16)) << 4));
             v4f t = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int m = 0; m < 4; ++m)
-              t = mfma_bf16_16x16x32(int4x8_bias128((uint32_t)wq[m]), *(const v8s*)(trow + ks * 256 + m * 16), t);
+              t = mfma_bf16_16x16x32(int4x8_bias128((uint32_t)wq[m], w4k), *(const v8s*)(trow + ks * 256 + m * 16), t);
             // sum (u - 8) x = sum (u + 128) x - 136 sum x, then the row's scale
             // (q * s is exact in bf16, so scaling after the sum is the
             // bf16(q * s) weight's product).
             const float bias = 136.f * tsc[ks];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const uint32_t two = (uint32_t)sc4[r];
-              const float sr = bf16_bits_to_f32((uint16_t)(kk == 0 ? two & 0xffffu : two >> 16));
+              // Row r's scale of K-step kk: half kk % 2 of dword r W4_PR + kk / 2.
+              const int dw = r * W4_PR + (kk >> 1);
+              const uint32_t two = (uint32_t)sc4[dw >> 2][dw & 3];
+              const float sr = bf16_bits_to_f32((uint16_t)((kk & 1) == 0 ? two & 0xffffu : two >> 16));
               acc[r] += (t[r] - bias) * sr;
             }
           }
@@ -998,7 +1036,7 @@ static int run_stream_fp8_cu(const GemmArgs& a, int cap, size_t shmem, hipStream
     }
     attr_bytes = shmem;
   }
-  kern<<<dim3(num_cu()), dim3(kCuThreads), shmem, stream>>>(a, cap);
+  kern<<<dim3(num_cu()), dim3(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads), shmem, stream>>>(a, cap);
   return launch_status("stream_fp8_cu");
 }
 
@@ -1012,11 +1050,13 @@ static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, in
   if (int4 && (KS % 2 != 0 || a.a_scale)) return false;
   // Rows staged per window: as many as the LDS budget allows.
   // 1 KB stays free for the kernel's static LDS.
-  const size_t fixed = cu_sc_off<KS>(a.num_experts, a.M) + 16 + 1024;
+  const size_t fixed = (int4 ? cu_sc_off<KS, true>(a.num_experts, a.M) : cu_sc_off<KS>(a.num_experts, a.M)) +
+                       16 + 1024;
   if (fixed + 4 * per_row > kCuLdsMax) return false;  // windows need a few rows
   int cap = (int)((kCuLdsMax - fixed) / per_row);
   if (cap > 1024) cap = 1024;
-  const size_t shmem = cu_rows_off<KS>(a.num_experts, a.M, cap) + (size_t)cap * cu_pitch<KS>();
+  const size_t shmem = (int4 ? cu_rows_off<KS, true>(a.num_experts, a.M, cap)
+                             : cu_rows_off<KS>(a.num_experts, a.M, cap)) + (size_t)cap * cu_pitch<KS>();
   if constexpr (KS % 2 == 0) {
     if (int4) {
       *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_W4>(a, cap, shmem, stream)
