@@ -61,10 +61,12 @@ struct Plan {
   // reduced, the down output) are stored by sorted position, so every tile
   // reads and writes contiguous rows; the top-k sum gathers through pos_of.
   bool by_pos = false;
+  // W4A16 above decode size: the 64-token int4 tile GEMM (gemm_w4.hip).
+  bool w4_tile = false;
   int bm = 16;
   int64_t slots = 0, max_padded = 0, max_blocks = 0;
   size_t off_sorted, off_eids, off_ntpp, off_eoff, off_ecnt, off_c2, off_c3, off_hq, off_hs,
-      off_cq, off_cs, off_scratch, scratch_bytes, off_tw, off_ids, off_pos, total;
+      off_cq, off_cs, off_scratch, scratch_bytes, off_tw, off_ids, off_pos, off_w4h, off_w4hx, off_w4cx, total;
 };
 
 // with_route: the plan also holds the router outputs and the routing scratch
@@ -97,7 +99,8 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->ids_mode = pl->stream && pl->slots <= kStreamMaxIdsSlots &&
                  (quant == MSTAR_QUANT_FP8_W8A8 ||
                   (quant == MSTAR_QUANT_W4A16 && H % 256 == 0 && I % 256 == 0));
-  pl->bm = pl->stream ? 16 : choose_bm(pl->slots, E, quant == MSTAR_QUANT_FP8_W8A8);
+  pl->w4_tile = quant == MSTAR_QUANT_W4A16 && !pl->stream && w4_tile_supported(H, I);
+  pl->bm = pl->stream ? 16 : pl->w4_tile ? 64 : choose_bm(pl->slots, E, quant == MSTAR_QUANT_FP8_W8A8);
   pl->max_padded = pl->slots + (int64_t)E * (pl->bm - 1);
   pl->max_blocks = (pl->max_padded + pl->bm - 1) / pl->bm;
   size_t o = 0;
@@ -125,6 +128,11 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->off_cq = fp8_tiled ? take(cq_rows * I) : 0;
   pl->off_cs = fp8_tiled ? take(cq_rows * (I / 128) * 4) : 0;
   pl->off_pos = pl->by_pos ? take((size_t)pl->slots * 4) : 0;
+  // W4 tiles: hidden rows in pair order and their group sums, and the group
+  // sums of the gate_up output.
+  pl->off_w4h = pl->w4_tile ? take((size_t)M * H * 2) : 0;
+  pl->off_w4hx = pl->w4_tile ? take((size_t)M * (H / 128) * 4) : 0;
+  pl->off_w4cx = pl->w4_tile ? take((size_t)pl->slots * (I / 128) * 4) : 0;
   pl->scratch_bytes = with_route ? route_scratch_bytes(M, top_k, E) : align_scratch_bytes(pl->slots, E);
   pl->off_scratch = take(pl->scratch_bytes);
   pl->off_tw = with_route ? take((size_t)pl->slots * 4) : 0;
@@ -236,6 +244,17 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
     }
     g2.A = cq; g2.lda = I; g2.a_scale = cs; g2.ld_as = I / 128;
     st = launch_tile_gemm(g2, A_FP8G, B_FP8BLK, EPI_STORE, act_dtype, true, pl.bm, stream);
+    if (st != kOk) return st;
+  } else if (pl.w4_tile) {
+    uint16_t* hp = (uint16_t*)(ws + pl.off_w4h);
+    float* hx = (float*)(ws + pl.off_w4hx);
+    float* cx = (float*)(ws + pl.off_w4cx);
+    st = launch_w4_prep(hidden, H, M, H, hp, hx, stream);
+    if (st != kOk) return st;
+    g1.A = hp; g1.lda = H;
+    st = launch_w4_tile(g1, EPI_ACT, hx, cx, stream);
+    if (st != kOk) return st;
+    st = launch_w4_tile(g2, EPI_STORE, cx, nullptr, stream);
     if (st != kOk) return st;
   } else {
     g1.A = hidden; g1.lda = H;

@@ -267,14 +267,14 @@ __device__ __forceinline__ Int4BiasConsts int4_bias_consts() {
   asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(k.c));
   return k;
 }
+// The bit-field insert is written in C (the compiler selects v_bfi_b32 and,
+// unlike for inline assembly, inserts the wait states an MFMA reading its
+// result needs); the constants are opaque so that it is not folded into an
+// and and an or.
 __device__ __forceinline__ v8s int4x8_bias128(uint32_t w, Int4BiasConsts k) {
   v4i r;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t y;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(y) : "s"(k.m), "v"(w >> (4 * j)), "v"(k.c));
-    r[j] = (int)y;
-  }
+  for (int j = 0; j < 4; ++j) r[j] = (int)(((w >> (4 * j)) & k.m) | (k.c & ~k.m));
   return __builtin_bit_cast(v8s, r);
 }
 

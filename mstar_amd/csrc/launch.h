@@ -137,6 +137,17 @@ bool stream_gemm_supported(int K, int max_rows, int akind, int bkind);
 // int4 weights (group-128 bf16 scales) and bf16 token rows.
 int launch_stream_int4_cu(const GemmArgs& a, int epi, hipStream_t stream);
 int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t stream);
+// gemm_w4.hip: W4A16 grouped GEMM over alignment blocks of 64 tokens.  Token
+// rows (A) are stored in the int4 codes' pair order (each 8-group holds
+// elements 0, 4, 1, 5, 2, 6, 3, 7) with fp32 sums per 128-group (xs,
+// [rows, K / 128]).  EPI_ACT writes C in that order and the sums of its
+// groups (xs_out, [slots, inter / 128]) for the down GEMM.
+bool w4_tile_supported(int64_t H, int64_t I);
+int launch_w4_tile(const GemmArgs& a, int epi, const float* xs, float* xs_out, hipStream_t stream);
+// Hidden rows [rows, H] (row stride ldx) -> pair order [rows, H] and the
+// group sums [rows, H / 128].
+int launch_w4_prep(const void* x, int64_t ldx, int64_t rows, int64_t H, void* out, float* xs,
+                   hipStream_t stream);
 constexpr int kBigBlockM = 256;
 
 // stream_fp8.hip: persistent FP8 weight streaming (bf16 activations,

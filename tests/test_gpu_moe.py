@@ -314,11 +314,12 @@ def test_layer_under_hip_graph_replays():
 @pytest.mark.parametrize("M,bias,quant", [(32, False, "fp8_w8a8"), (8, False, "fp8_w8a8"),
                                           (512, True, "fp8_w8a8"), (1024, True, "fp8_w8a8"),
                                           (4096, True, "fp8_w8a8"), (16, False, None),
-                                          (32, False, "w4a16")])
+                                          (32, False, "w4a16"), (1024, True, "w4a16")])
 def test_moe_layer_from_logits(M, bias, quant):
     """Routing from logits + experts in one library call (mstar_moe_layer).
     From 4096 slots up the multi-workgroup routing also quantises the hidden
-    rows; at M=4096 the 256-row FP8 tile kernel runs."""
+    rows; at M=4096 the 256-row FP8 tile kernel runs; W4A16 at M=1024 (Zipf
+    routing: experts spanning many 64-token blocks) runs the int4 tile GEMM."""
     from mstar_amd import _lib, ops, quant as Q
     H, E, I, k = 2048, 128, 768, 8
     x = _hidden(M, H, seed=M + 21)
