@@ -190,6 +190,28 @@ def test_fused_experts_fp8_bm128_path():
     assert_moe_close(out, _fp8_ref(x, q1, s1, q2, s2, tw, ti), what="fp8 bm128")
 
 
+@pytest.mark.parametrize("H,I,E,k,M", [(256, 256, 4, 2, 200), (512, 256, 8, 1, 100), (256, 512, 2, 2, 130),
+                                       (2048, 768, 128, 8, 65)])
+def test_fused_experts_w4a16_tile_shapes(H, I, E, k, M):
+    """The int4 tile GEMM at its edges: one K-step per tile (the next tile's
+    first step issued in the same iteration), a single n-tile, top-1, fewer
+    tiles than CUs, and the smallest token count above the streaming path."""
+    from mstar_amd import quant
+    from mstar_amd.fused_moe import fused_experts
+    w1, w2 = _weights(H, E, I, seed=H + I + E)
+    p1, t1 = quant.quantize_int4_group(w1)
+    p2, t2 = quant.quantize_int4_group(w2)
+    x = _hidden(M, H, seed=M + E)
+    tw, ti = _routing(M, E, k, seed=M + k)
+    out = fused_experts(x.to(DEV), p1, p2, tw.to(DEV), ti.to(DEV), quant="w4a16",
+                        w1_scale=t1, w2_scale=t2)
+    p1c, t1c, p2c, t2c = p1.cpu(), t1.cpu(), p2.cpu(), t2.cpu()
+    ref = O.fused_experts_rounding(x, None, None, tw, ti,
+                                   w1_dq=lambda e: O.dequant_int4_group(p1c[e], t1c[e]),
+                                   w2_dq=lambda e: O.dequant_int4_group(p2c[e], t2c[e]))
+    assert_moe_close(out, ref, what=f"w4a16 tile H={H} I={I} E={E} k={k} M={M}")
+
+
 def test_weight_quant_matches_oracle():
     from mstar_amd import quant
     w1, _ = _weights(256, 4, 128, seed=8)
