@@ -411,6 +411,10 @@ int mstar_fp8_scaled_mm(const uint8_t* a, const float* a_scale, const uint8_t* w
   g.B = w; g.ldb = K; g.b_estride = 0; g.b_scale = w_scale;
   g.C = out; g.ldc = N;
   g.M = M; g.N = (int)N; g.K = (int)K; g.top_k = 1;
+  if (dense_stream_supported(M, N, K)) {
+    const int st = launch_dense_stream(g, (hipStream_t)stream);
+    if (st != kUnsupported) return st;  // else the tile kernel below
+  }
   const int bm = M <= 32 ? 32 : M <= 64 ? 64 : kBigBlockM;
   return launch_tile_gemm(g, A_FP8R, B_FP8R, EPI_DENSE, kBF16, false, bm, (hipStream_t)stream);
 }

@@ -142,6 +142,10 @@ int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t st
 // elements 0, 4, 1, 5, 2, 6, 3, 7) with fp32 sums per 128-group (xs,
 // [rows, K / 128]).  EPI_ACT writes C in that order and the sums of its
 // groups (xs_out, [slots, inter / 128]) for the down GEMM.
+// gemm_dense.hip: per-token x per-channel FP8 GEMM for M <= 32 (weights
+// streamed once; persistent, one workgroup per CU).
+bool dense_stream_supported(int64_t M, int64_t N, int64_t K);
+int launch_dense_stream(const GemmArgs& a, hipStream_t stream);
 bool w4_tile_supported(int64_t H, int64_t I);
 int launch_w4_tile(const GemmArgs& a, int epi, const float* xs, float* xs_out, hipStream_t stream);
 // Hidden rows [rows, H] (row stride ldx) -> pair order [rows, H] and the

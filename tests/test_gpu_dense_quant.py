@@ -59,6 +59,18 @@ def test_fp8_scaled_mm_vs_oracle(M, N):
     assert_moe_close(out, ref, what=f"fp8_scaled_mm {M}x{N}")
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 2048), (7, 2064, 2048), (16, 2048, 256), (17, 4112, 1024),
+                                   (32, 1040, 512)])
+def test_fp8_scaled_mm_decode_stream(M, N, K):
+    """M <= 32 runs the weight-streaming kernel: one and two token subtiles,
+    channel counts that do not split evenly over the CUs, short K."""
+    from mstar_amd import ops
+    aq, as_, wq, ws = _dense(M, N, K, seed=M + N + K)
+    out = ops.fp8_scaled_mm(aq, as_, wq, ws)
+    ref = O.fp8_scaled_mm(aq.cpu(), as_.cpu(), wq.cpu(), ws.cpu())
+    assert_moe_close(out, ref, what=f"fp8_scaled_mm stream {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("M", [32, 4096])
 def test_fp8_scaled_mm_lm_head(M):
     """N = 151936 (the vocabulary projection of config 4)."""
