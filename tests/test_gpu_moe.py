@@ -101,6 +101,41 @@ def test_fused_experts_fp16_gelu_unreduced():
     assert_moe_close(out, ref, what="fp16 gelu unreduced")
 
 
+@pytest.mark.parametrize("quant,M", [("fp8_w8a8", 32), ("fp8_w8a8", 300), ("fp8_w8a8", 4096),
+                                     ("w4a16", 32), ("w4a16", 300)])
+@pytest.mark.parametrize("reduce", [True, False])
+def test_fused_experts_quantised_gelu(quant, M, reduce):
+    """GeLU (tanh) through every quantised path -- decode streaming (M=32),
+    mid-size tiles (M=300: FP8 128-row tiles, int4 64x256 tiles) and the
+    256-row FP8 kernel (M=4096) -- with and without the top-k sum."""
+    from mstar_amd import quant as Q
+    from mstar_amd.fused_moe import fused_experts
+    H, E, I, k = 2048, 128, 768, 8
+    x = _hidden(M, H, seed=M + 7)
+    tw, ti = _routing(M, E, k, seed=M + 7)
+    if quant == "fp8_w8a8":
+        q1, s1, q2, s2 = _fp8_weights(H, E, I)
+        c1, c2, c3, c4 = q1.cpu(), s1.cpu(), q2.cpu(), s2.cpu()
+        d1 = lambda e: O.dequant_fp8_block(c1[e], c2[e])
+        d2 = lambda e: O.dequant_fp8_block(c3[e], c4[e])
+        kw = dict(block_shape=(128, 128))
+        aq = True
+    else:
+        w1, w2 = _weights(H, E, I)
+        q1, s1 = Q.quantize_int4_group(w1)
+        q2, s2 = Q.quantize_int4_group(w2)
+        c1, c2, c3, c4 = q1.cpu(), s1.cpu(), q2.cpu(), s2.cpu()
+        d1 = lambda e: O.dequant_int4_group(c1[e], c2[e])
+        d2 = lambda e: O.dequant_int4_group(c3[e], c4[e])
+        kw = {}
+        aq = False
+    out = fused_experts(x.to(DEV), q1, q2, tw.to(DEV), ti.to(DEV), activation="gelu",
+                        reduce_results=reduce, quant=quant, w1_scale=s1, w2_scale=s2, **kw)
+    ref = O.fused_experts_rounding(x, None, None, tw, ti, activation="gelu", reduce_results=reduce,
+                                   w1_dq=d1, w2_dq=d2, act_quant=aq)
+    assert_moe_close(out, ref, what=f"{quant} gelu M={M} reduce={reduce}")
+
+
 def test_reference_api_composition():
     """The reference runner's own sequence (runner.py:99-159) through the
     drop-in kernel entry points: align -> GEMM1 -> act_and_mul -> GEMM2 ->
