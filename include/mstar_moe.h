@@ -118,12 +118,12 @@ int mstar_moe_align_scratch_size(int64_t numel, int num_experts, size_t* bytes);
 
 /* Softmax top-k + alignment in one call: mstar_moe_topk_softmax followed by
  * mstar_moe_align_block_size on its ids (one launch when
- * num_tokens*top_k <= 4096, else two).  Replaces the router's
+ * num_tokens*top_k <= 512, else two).  Replaces the router's
  * softmax/topk/renormalise (mstar/model/components/moe.py:131-139) plus
  * moe_align_block_size (mstar/utils/fused_moe/align.py:55-103) as the
  * reference runs them back to back.  topk_ids_i32 and topk_ids_i64 may be
  * NULL (the int32 ids then live in scratch).  scratch: see
- * mstar_moe_route_scratch_size (required above 4096 slots). */
+ * mstar_moe_route_scratch_size (required above 512 slots). */
 int mstar_moe_route(const void* router_logits, int logits_dtype, int64_t num_tokens,
                     int num_experts, int top_k, int renormalize, float* topk_weights,
                     int32_t* topk_ids_i32, int64_t* topk_ids_i64, int block_size,

@@ -79,7 +79,12 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict_
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kAlignBatch = 16;          // ids held per lane per batch
-constexpr int kRouteSmallSlots = 4096;   // numel served by one workgroup
+constexpr int kRouteSmallSlots = 4096;   // numel aligned by one workgroup
+// Slots routed (top-k + alignment) by one workgroup.  The top-k costs about
+// 500 VALU instructions per token, so one CU is the bottleneck beyond a few
+// dozen tokens: 512 tokens took 115 us in one workgroup against 26 us over
+// the grid-wide path (whose first pass also quantises the hidden rows).
+constexpr int kRouteTopkSmallSlots = 512;
 constexpr int kRouteTokensPerBlock = 32;  // 256 workgroups at 8192 tokens
 
 // Expert of slot i, or E for "skip" (out of range / beyond the end).
@@ -517,7 +522,7 @@ size_t align_scratch_bytes(int64_t numel, int E) {
   return (size_t)(blocks > 0 ? blocks : 1) * E * sizeof(int32_t);
 }
 
-bool route_is_grid(int64_t M, int k) { return M * k > kRouteSmallSlots; }
+bool route_is_grid(int64_t M, int k) { return M * k > kRouteTopkSmallSlots; }
 
 size_t route_scratch_bytes(int64_t M, int k, int E) {
   const int64_t blocks = (M + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock;
@@ -585,7 +590,7 @@ static int route_impl(const void* logits, int64_t M, int E, int k, int renorm, f
                       float* hs) {
   const int64_t numel = M * k;
   int st;
-  if (numel <= kRouteSmallSlots) {
+  if (numel <= kRouteTopkSmallSlots) {
     const size_t shmem = sizeof(int) * (size_t)((numel + 3) & ~3ll) + single_lds(E);
     static size_t done = 0;
     if ((st = opt_in_lds(route_small_kernel<LT, EPL>, shmem, done)) != kOk) return st;

@@ -106,7 +106,9 @@ def test_align_all_tokens_one_expert():
 
 @pytest.mark.parametrize("M,E,k,bm,bias,dt", [
     (32, 128, 8, 16, False, torch.float32),      # decode: one launch
-    (512, 128, 8, 64, True, torch.float32),      # exactly 4096 slots: one launch
+    (64, 128, 8, 32, True, torch.float32),       # exactly 512 slots: one launch
+    (65, 128, 8, 32, True, torch.float32),       # 520 slots: grid path, one ragged block
+    (512, 128, 8, 64, True, torch.float32),      # 4096 slots: grid path, 16 blocks
     (600, 128, 8, 64, True, torch.float32),      # grid path, ragged last block
     (8192, 128, 8, 64, True, torch.float32),     # config 3 prefill
     (1000, 64, 6, 32, False, torch.bfloat16),    # bf16 logits (ties), k=6
