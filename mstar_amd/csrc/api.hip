@@ -37,12 +37,17 @@ int launch_status(const char* what) {
 static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Row block for the tiled grouped GEMM: about one block per expert's share of
-// the slots, so padding stays a small fraction of the work.
+// the slots, so padding stays a small fraction of the work.  FP8 goes to the
+// persistent 256-row kernel from 24 slots per expert on average: despite the
+// padding it matches the 32/64-row tiles at 512 and 1024 tokens (E=128, top-8)
+// and beats them at 2048 (gate_up + down 177 against 242 us), because the
+// one-tile-per-workgroup kernel spends most of the down GEMM's 6 K-steps
+// filling its pipeline, and its gate_up epilogue quantises in place.
 static int choose_bm(int64_t slots, int E, bool fp8) {
   const int64_t avg = slots / (E > 0 ? E : 1);
+  if (fp8 && avg >= 24) return kBigBlockM;
   if (avg <= 48) return 32;
   if (avg <= 160) return 64;
-  if (fp8 && avg >= 256) return kBigBlockM;
   return 128;
 }
 

@@ -374,8 +374,8 @@ def test_layer_under_hip_graph_replays():
                                           (32, False, "w4a16"), (1024, True, "w4a16")])
 def test_moe_layer_from_logits(M, bias, quant):
     """Routing from logits + experts in one library call (mstar_moe_layer).
-    From 4096 slots up the multi-workgroup routing also quantises the hidden
-    rows; at M=4096 the 256-row FP8 tile kernel runs; W4A16 at M=1024 (Zipf
+    Above 512 slots the multi-workgroup routing also quantises the hidden
+    rows; from M=384 (24 slots per expert) the 256-row FP8 tile kernel runs; W4A16 at M=1024 (Zipf
     routing: experts spanning many 64-token blocks) runs the int4 tile GEMM."""
     from mstar_amd import _lib, ops, quant as Q
     H, E, I, k = 2048, 128, 768, 8
@@ -431,7 +431,7 @@ def test_moe_layer_decode_bf16_logits(M, renorm, E, k):
 
 @pytest.mark.parametrize("M,E,k,H,I,bias", [(1024, 16, 4, 512, 256, False), (2048, 32, 8, 1024, 384, True)])
 def test_fused_experts_fp8_big_tile_path(M, E, k, H, I, bias):
-    """>= 256 slots per expert on average selects the 256 x 256 FP8 tile kernel."""
+    """>= 24 slots per expert on average selects the 256 x 256 FP8 tile kernel."""
     from mstar_amd.fused_moe import fused_experts
     q1, s1, q2, s2 = _fp8_weights(H, E, I, seed=9)
     x = _hidden(M, H, seed=9)
