@@ -85,7 +85,15 @@ constexpr int kRouteSmallSlots = 4096;   // numel aligned by one workgroup
 // dozen tokens: 512 tokens took 115 us in one workgroup against 26 us over
 // the grid-wide path (whose first pass also quantises the hidden rows).
 constexpr int kRouteTopkSmallSlots = 512;
-constexpr int kRouteTokensPerBlock = 32;  // 256 workgroups at 8192 tokens
+// Tokens per workgroup of the grid-wide routing: about 256 workgroups, 8 to
+// 32 tokens each.  Fewer tokens per workgroup spread the top-k and the hidden
+// quantisation over more CUs (512 tokens: 14 us at 8 per workgroup, 27 us at
+// 32), but the scatter pass scans every earlier workgroup's histogram, so
+// beyond about 256 workgroups it grows (8192 tokens at 8: 45 us of scatter).
+static int route_tokens_per_block(int64_t M) {
+  const int64_t t = (M + 255) / 256;
+  return t < 8 ? 8 : t > 32 ? 32 : (int)t;
+}
 
 // Expert of slot i, or E for "skip" (out of range / beyond the end).
 template <typename IT>
@@ -294,7 +302,7 @@ __global__ __launch_bounds__(kAlignThreads) void route_small_kernel(
 }
 
 // ---- grid-wide path --------------------------------------------------------
-// Pass 1 (top-k variant): top-k of kRouteTokensPerBlock tokens per workgroup
+// Pass 1 (top-k variant): top-k of `tpb` tokens per workgroup
 // and the workgroup's expert histogram hist[b][E].  With `hidden` (bf16
 // [M, H], H % 128 == 0) the workgroup also quantises its tokens' hidden rows
 // per group of 128 into e4m3fn codes hq [M, H] and scales hs [M, H/128].
@@ -303,14 +311,14 @@ __global__ __launch_bounds__(kAlignThreads) void topk_hist_kernel(
     const LT* __restrict__ logits, int64_t M, int E, int k, int renorm, float* __restrict__ w_out,
     int32_t* __restrict__ ids32, int64_t* __restrict__ ids64, int32_t* __restrict__ hist,
     const uint16_t* __restrict__ hidden, int64_t H, uint8_t* __restrict__ hq,
-    float* __restrict__ hs) {
+    float* __restrict__ hs, int tpb) {
   extern __shared__ int smem[];
   int* h = smem;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int e = threadIdx.x; e < E; e += kAlignThreads) h[e] = 0;
   __syncthreads();
-  const int64_t t0 = (int64_t)blockIdx.x * kRouteTokensPerBlock;
-  const int64_t t1 = t0 + kRouteTokensPerBlock < M ? t0 + kRouteTokensPerBlock : M;
+  const int64_t t0 = (int64_t)blockIdx.x * tpb;
+  const int64_t t1 = t0 + tpb < M ? t0 + tpb : M;
   topk_tokens<LT, EPL>(logits, t0 + w, t1, kAlignWaves, E, k, renorm, lane,
                        [&](int64_t t, int r, int id, float wt) {
                          w_out[t * k + r] = wt;
@@ -525,7 +533,8 @@ size_t align_scratch_bytes(int64_t numel, int E) {
 bool route_is_grid(int64_t M, int k) { return M * k > kRouteTopkSmallSlots; }
 
 size_t route_scratch_bytes(int64_t M, int k, int E) {
-  const int64_t blocks = (M + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock;
+  const int tpb = route_tokens_per_block(M);
+  const int64_t blocks = (M + tpb - 1) / tpb;
   return (size_t)(blocks > 0 ? blocks : 1) * E * sizeof(int32_t) + (size_t)M * k * sizeof(int32_t);
 }
 
@@ -604,16 +613,17 @@ static int route_impl(const void* logits, int64_t M, int E, int k, int renorm, f
                    route_scratch_bytes(M, k, E));
     return kWorkspaceTooSmall;
   }
-  const int nblocks = (int)((M + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock);
+  const int tpb = route_tokens_per_block(M);
+  const int nblocks = (int)((M + tpb - 1) / tpb);
   int32_t* hist = (int32_t*)scratch;
   int32_t* tmp_ids = ids32 ? ids32 : hist + (size_t)nblocks * E;
   topk_hist_kernel<LT, EPL><<<nblocks, kAlignThreads, E * sizeof(int), stream>>>(
-      (const LT*)logits, M, E, k, renorm, w, tmp_ids, ids64, hist, hidden, H, hq, hs);
+      (const LT*)logits, M, E, k, renorm, w, tmp_ids, ids64, hist, hidden, H, hq, hs, tpb);
   const size_t sshm = scatter_lds(E);
   static size_t done = 0;
   if ((st = opt_in_lds(scatter_kernel<GlobalIds<int32_t>>, sshm, done)) != kOk) return st;
   scatter_kernel<<<nblocks, kAlignThreads, sshm, stream>>>(
-      GlobalIds<int32_t>{tmp_ids}, numel, E, bm, kRouteTokensPerBlock * k, nblocks, hist,
+      GlobalIds<int32_t>{tmp_ids}, numel, E, bm, tpb * k, nblocks, hist,
       sorted_ids, expert_ids, ntpp, max_padded, expert_off, expert_cnt);
   return launch_status("moe_route");
 }

@@ -110,7 +110,8 @@ def test_align_all_tokens_one_expert():
     (65, 128, 8, 32, True, torch.float32),       # 520 slots: grid path, one ragged block
     (512, 128, 8, 64, True, torch.float32),      # 4096 slots: grid path, 16 blocks
     (600, 128, 8, 64, True, torch.float32),      # grid path, ragged last block
-    (8192, 128, 8, 64, True, torch.float32),     # config 3 prefill
+    (8192, 128, 8, 64, True, torch.float32),     # config 3 prefill (32 tokens per workgroup)
+    (5000, 128, 8, 64, True, torch.float32),     # 20 tokens per workgroup, ragged last block
     (1000, 64, 6, 32, False, torch.bfloat16),    # bf16 logits (ties), k=6
     (3, 8, 2, 64, False, torch.float32),
 ])
