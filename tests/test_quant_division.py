@@ -1,4 +1,6 @@
-"""The prefill gate_up epilogue divides by the FP8 group scale as
+"""The FP8 group quantisers (the prefill gate_up epilogue, and the
+per-token-group quantiser of hidden rows used by routing, the standalone
+quantiser and the decode kernels' staging) divide by the group scale as
 y = x * r, r = 1/scale (IEEE), then y + fma(-y, scale, x) * r.  This checks,
 in emulated fp32 (products of two fp32 values are exact in float64, as the
 FMA's are), that the corrected quotient equals IEEE fp32 division for the
