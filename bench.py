@@ -69,6 +69,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-extra", action="store_true", help="skip the config 4 / 5 lines")
+    p.add_argument("--no-sweep", action="store_true",
+                   help="skip the prefill M=512/2048 and dense N=4096/2048 lines (profiler runs)")
     p.add_argument("--kernel-only", action="store_true",
                    help="launch only the gate_up GEMM in a loop (for profiler runs)")
     return p.parse_args()
@@ -206,7 +208,8 @@ def dense_fp8_lines(args, K=2048):
         return res
 
     res = one_n(151936)
-    res["other_N"] = {f"N{N}": one_n(N) for N in (4096, 2048)}
+    if not args.no_sweep:
+        res["other_N"] = {f"N{N}": one_n(N) for N in (4096, 2048)}
     res["workload"] = f"config 4: [M, {K}] x [N, {K}]^T, per-token x per-channel e4m3fn, N=151936 at top level"
     return res
 
@@ -356,7 +359,7 @@ def main():
         del gp
         # The rest of config 3's shape sweep (M = 512, 2048), same routing bias.
         sweep = []
-        for Ms in (512, 2048):
+        for Ms in (() if args.no_sweep else (512, 2048)):
             xs, ls = make_inputs(Ms, bias=True, seed=3)
             gs, _ = capture(lambda: layer(xs, ls, base))
             ssec = time_graphs([gs], max(20, args.steps // 5), 3)
@@ -364,7 +367,8 @@ def main():
             sweep.append({"tokens": Ms, "us": round(ssec * 1e6, 1), "TFLOPs": round(tfs, 1),
                           "mfma_fp8_frac": round(tfs / FP8_PEAK_TFLOPS, 4)})
             del gs
-        out["prefill_sweep"] = sweep
+        if sweep:
+            out["prefill_sweep"] = sweep
 
     if not args.no_extra:
         del weights, graphs
