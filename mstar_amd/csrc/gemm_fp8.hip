@@ -294,6 +294,11 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     const int t = tile_of(j);
     const int mb = mb_of(t), nt = nt_of(t);
     const int buf = j % kBigIdBufs;
+    // A block's padding rows are a suffix (one expert per block), so a wave
+    // whose first token row is padding has no rows at all: it skips its
+    // fragment reads, MFMAs and promotion, but still issues its share of the
+    // DMA (fixed per-wave counts) and meets every barrier.  Wave-uniform.
+    const bool live = __builtin_amdgcn_readfirstlane(slot_of(t, buf, wm * WTM)) >= 0;
     // acc[i][j]: the transposed 32x32 tile (weight rows x token columns).
     v16f acc[MB][NB];
 #pragma unroll
@@ -320,6 +325,11 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
       const uint8_t* st = smem + (q % kBigStages) * kBigStageBytes;
       const uint8_t* sA = st;
       const uint8_t* sB = st + BM * 128;
+      if (!live) {
+#pragma unroll
+        for (int n = 0; n < kParts; ++n) issue_part(n, ik, ist);
+        continue;
+      }
       // Token fragments of both row tiles stay in registers for the step;
       // weight fragments stream one 32-row tile at a time.
       v8i x[MB][2];
