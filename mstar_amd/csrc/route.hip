@@ -289,13 +289,15 @@ __global__ __launch_bounds__(kAlignThreads) void route_small_kernel(
   int* sIds = smem;                         // [M * k]
   int* rest = sIds + ((M * k + 3) & ~3ll);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  topk_tokens<LT, EPL>(logits, w, M, kAlignWaves, E, k, renorm, lane,
-                       [&](int64_t t, int r, int id, float wt) {
-                         w_out[t * k + r] = wt;
-                         sIds[t * k + r] = id;
-                         if (ids32) ids32[t * k + r] = id;
-                         if (ids64) ids64[t * k + r] = id;
-                       });
+  const auto put = [&](int64_t t, int r, int id, float wt) {
+    w_out[t * k + r] = wt;
+    sIds[t * k + r] = id;
+    if (ids32) ids32[t * k + r] = id;
+    if (ids64) ids64[t * k + r] = id;
+  };
+  // Four tokens per wave (one per 16-lane row) when the experts fit a row.
+  if (EPL <= 4 && k <= 16) topk_tokens_rows<LT, 4 * EPL>(logits, 0, M, w, kAlignWaves, E, k, renorm, lane, put);
+  else topk_tokens<LT, EPL>(logits, w, M, kAlignWaves, E, k, renorm, lane, put);
   __syncthreads();
   single_block_align(rest, M * k, E, bm, max_padded, sorted_ids, expert_ids, ntpp, expert_off,
                      expert_cnt, LdsIds{sIds});
@@ -319,13 +321,14 @@ __global__ __launch_bounds__(kAlignThreads) void topk_hist_kernel(
   __syncthreads();
   const int64_t t0 = (int64_t)blockIdx.x * tpb;
   const int64_t t1 = t0 + tpb < M ? t0 + tpb : M;
-  topk_tokens<LT, EPL>(logits, t0 + w, t1, kAlignWaves, E, k, renorm, lane,
-                       [&](int64_t t, int r, int id, float wt) {
-                         w_out[t * k + r] = wt;
-                         ids32[t * k + r] = id;
-                         if (ids64) ids64[t * k + r] = id;
-                         atomicAdd(&h[id], 1);
-                       });
+  const auto put = [&](int64_t t, int r, int id, float wt) {
+    w_out[t * k + r] = wt;
+    ids32[t * k + r] = id;
+    if (ids64) ids64[t * k + r] = id;
+    atomicAdd(&h[id], 1);
+  };
+  if (EPL <= 4 && k <= 16) topk_tokens_rows<LT, 4 * EPL>(logits, t0, t1, w, kAlignWaves, E, k, renorm, lane, put);
+  else topk_tokens<LT, EPL>(logits, t0 + w, t1, kAlignWaves, E, k, renorm, lane, put);
   if (hidden) {
     // 8-element chunks of the block's rows; 16 consecutive chunks (16
     // lanes) form one group of 128.

@@ -112,4 +112,84 @@ __device__ __forceinline__ void topk_tokens(const LT* __restrict__ logits, int64
   }
 }
 
+// Minimum over a 16-lane row by DPP row rotations (every lane gets it).
+__device__ __forceinline__ uint32_t row_umin16(uint32_t v) {
+  v = min(v, (uint32_t)dpp_row_ror<1>((int)v));
+  v = min(v, (uint32_t)dpp_row_ror<2>((int)v));
+  v = min(v, (uint32_t)dpp_row_ror<4>((int)v));
+  v = min(v, (uint32_t)dpp_row_ror<8>((int)v));
+  return v;
+}
+
+// Softmax top-k of one token per 16-lane row (four tokens per wave), for
+// E <= 16 * EPR and k <= 16: expert e in row lane e % 16, slot e / 16.
+// The same selection as topk_wave -- k rounds of argmax over the
+// order-preserving keys, ties to the lower expert index -- with row-wide
+// DPP reductions, so a wave ranks four tokens at the instruction cost of
+// about one.  The softmax sum is row lane 0's, broadcast to the row.
+// emit(rank, expert, weight) runs on row lane `rank` (< k); `active` false
+// rows (past the last token) take part in the reductions only.
+template <int EPR, typename Emit>
+__device__ __forceinline__ void topk_row16(const float (&v)[EPR], int E, int k, int renorm, int lane,
+                                           bool active, const Emit& emit) {
+  const int l16 = lane & 15;
+  uint32_t key[EPR];
+  float mxl = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < EPR; ++j) {
+    const bool valid = j * 16 + l16 < E;
+    key[j] = valid ? float_key(v[j]) : 0u;
+    mxl = fmaxf(mxl, valid ? v[j] : -INFINITY);
+  }
+  const float mx = row_fmax16(mxl);
+  float sl = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPR; ++j) sl += j * 16 + l16 < E ? __expf(v[j] - mx) : 0.f;
+  sl = row_fsum16(sl);  // row lane 0 holds the row's sum
+  const float s = __shfl(sl, lane & ~15, 64);
+  float my_p = 0.f, psum = 0.f;
+  int my_id = 0;
+  for (int r = 0; r < k; ++r) {
+    uint32_t lm = key[0];
+#pragma unroll
+    for (int j = 1; j < EPR; ++j) lm = max(lm, key[j]);
+    const uint32_t m = row_umax16(lm);
+    uint32_t cand = 0xffffffffu;
+#pragma unroll
+    for (int j = EPR - 1; j >= 0; --j)
+      if (key[j] == m) cand = (uint32_t)(j * 16 + l16);
+    const int sel = (int)row_umin16(cand);
+#pragma unroll
+    for (int j = 0; j < EPR; ++j)
+      if (sel == j * 16 + l16) key[j] = 0u;
+    const float p = __expf(key_float(m) - mx) / s;
+    psum += p;
+    if (l16 == r) {
+      my_p = p;
+      my_id = sel;
+    }
+  }
+  if (active && l16 < k) emit(l16, my_id, renorm ? my_p / psum : my_p);
+}
+
+// Top-k of tokens [tb, te) by the waves of a workgroup, four per wave at a
+// time (one per 16-lane row): wave w takes tokens tb + 4 (w + nw n) + row.
+// emit(token, rank, expert, weight).
+template <typename LT, int EPR, typename Emit>
+__device__ __forceinline__ void topk_tokens_rows(const LT* __restrict__ logits, int64_t tb, int64_t te, int w,
+                                                 int nw, int E, int k, int renorm, int lane, const Emit& emit) {
+  const int l16 = lane & 15, row = lane >> 4;
+  for (int64_t base = tb + 4 * (int64_t)w; base < te; base += 4 * (int64_t)nw) {
+    const int64_t t = base + row;
+    const bool active = t < te;
+    float v[EPR];
+#pragma unroll
+    for (int j = 0; j < EPR; ++j) {
+      const int e = j * 16 + l16;
+      v[j] = (active && e < E) ? load_logit<LT>(logits + t * E, e) : -INFINITY;
+    }
+    topk_row16<EPR>(v, E, k, renorm, lane, active, [&](int r, int id, float wt) { emit(t, r, id, wt); });
+  }
+}
+
 }  // namespace mstar
