@@ -80,10 +80,11 @@ constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kAlignBatch = 16;          // ids held per lane per batch
 constexpr int kRouteSmallSlots = 4096;   // numel aligned by one workgroup
-// Slots routed (top-k + alignment) by one workgroup.  The top-k costs about
-// 500 VALU instructions per token, so one CU is the bottleneck beyond a few
-// dozen tokens: 512 tokens took 115 us in one workgroup against 26 us over
-// the grid-wide path (whose first pass also quantises the hidden rows).
+// Slots routed (top-k + alignment) by one workgroup.  Set with the
+// one-token-per-wave top-k (about 500 VALU instructions per token), which
+// made one CU the bottleneck beyond a few dozen tokens: 512 tokens took
+// 115 us in one workgroup against 26 us over the grid-wide path (whose first
+// pass also quantises the hidden rows).
 constexpr int kRouteTopkSmallSlots = 512;
 // Tokens per workgroup of the grid-wide routing: about 256 workgroups, 8 to
 // 32 tokens each.  Fewer tokens per workgroup spread the top-k and the hidden
