@@ -1,7 +1,7 @@
-// Softmax top-k of one token per wave: shared by the routing kernels and
-// the decode gate_up kernel that routes in its prologue.  Restates
-// TopKRouter.forward (mstar/model/components/moe.py:131-139) from the
-// logits on.
+// Softmax top-k: one token per wave (the decode routing launch and the
+// fused router), or one token per 16-lane row (the grid-wide and
+// single-workgroup routing paths).  Restates TopKRouter.forward
+// (mstar/model/components/moe.py:131-139) from the logits on.
 #pragma once
 #include "common.h"
 
