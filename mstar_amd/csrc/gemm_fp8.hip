@@ -574,7 +574,12 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
             const int orw = orow((lr2 >> 5) * WTM + i * 32 + (lr2 & 31), slot_of(t, buf, (lr2 >> 5) * WTM + i * 32 + (lr2 & 31)));
             const int col = nt * BN + u * 8;
             const uint32_t off = orw >= 0 && col < p.N ? (uint32_t)(((int64_t)orw * p.ldc + col) * 2) : kOffNone;
-            __builtin_amdgcn_raw_buffer_store_b128(val, rs_c, off, 0, 0);
+            // Non-temporal stores: the dense output (1.24 GB at the LM-head
+            // shape) is not read here again, and the down GEMM's (268 MB at
+            // 8192 tokens) exceeds the last-level cache before the top-k sum
+            // reads it (measured: dense M=4096 4%, the 8192-token layer 1.6%
+            // faster).
+            __builtin_amdgcn_raw_buffer_store_b128(val, rs_c, off, 0, 2);
           }
           if (i + 1 < MB) lds_barrier();  // half i is read before half i + 1 lands
         }
