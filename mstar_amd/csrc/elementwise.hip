@@ -62,7 +62,12 @@ __global__ __launch_bounds__(256) void sum_reduce_kernel(const uint16_t* __restr
     for (int u = 0; u < 8; ++u) row[u] = POS ? (int64_t)pos_of[t * topk + j + u] : t * topk + j + u;
     v4i x[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = *(const v4i*)(in + row[u] * hidden + c);
+    for (int u = 0; u < 8; ++u) {
+      // By position (the 256-row prefill GEMM's output, stored non-temporally
+      // and read once): non-temporal loads too.
+      const v4i* src = (const v4i*)(in + row[u] * hidden + c);
+      x[u] = POS ? __builtin_nontemporal_load(src) : *src;
+    }
 #pragma unroll
     for (int u = 0; u < 8; ++u) add(x[u]);
   }
