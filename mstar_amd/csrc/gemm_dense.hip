@@ -165,7 +165,6 @@ __global__ __launch_bounds__(kDsThreads) void dense_stream_kernel(GemmArgs p, in
   wait_vmcnt<0>();  // no DMA outlives the kernel
 }
 
-static int g_ds_cus = 0;
 
 bool dense_stream_supported(int64_t M, int64_t N, int64_t K) {
   // K % 256: the token rows' pieces are swizzled within groups of 16.
@@ -179,31 +178,18 @@ bool dense_stream_supported(int64_t M, int64_t N, int64_t K) {
 
 template <int MS, int RING, int KC>
 static int run_dense_stream(const GemmArgs& a, hipStream_t stream) {
-  if (g_ds_cus <= 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&g_ds_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        g_ds_cus <= 0)
-      g_ds_cus = 256;
-  }
+  const int cus = device_cu_count();
   const int items = a.N / 16;
-  const int per = (items + g_ds_cus - 1) / g_ds_cus;
+  const int per = (items + cus - 1) / cus;
   const size_t shmem = ds_lds_bytes(RING, KC, MS, a.K);
   if (shmem > kDsLdsMax) {
     set_last_error("dense_stream: %zu bytes of LDS needed", shmem);
     return kUnsupported;
   }
   auto kern = dense_stream_kernel<MS, RING, KC>;
-  static size_t attr = 0;
-  if (shmem > attr) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem) !=
-        hipSuccess) {
-      set_last_error("dense_stream: cannot reserve %zu bytes of LDS", shmem);
-      return kLaunchError;
-    }
-    attr = shmem;
-  }
-  kern<<<dim3((unsigned)g_ds_cus), dim3(kDsThreads), shmem, stream>>>(a, per);
+  const int st = ensure_dynamic_lds((const void*)kern, shmem, "dense_stream");
+  if (st != kOk) return st;
+  kern<<<dim3((unsigned)cus), dim3(kDsThreads), shmem, stream>>>(a, per);
   return launch_status("dense_stream");
 }
 

@@ -609,24 +609,10 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
 template <int EPI, bool GROUPED, bool BLOCKSCALE>
 static int run_big(const GemmArgs& a, hipStream_t stream) {
   auto kern = gemm_fp8_big_kernel<EPI, GROUPED, BLOCKSCALE>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)kBigLds) != hipSuccess) {
-      set_last_error("gemm_fp8_big: cannot reserve %zu bytes of LDS", kBigLds);
-      return kLaunchError;
-    }
-    attr_set = true;
-  }
+  const int st = ensure_dynamic_lds((const void*)kern, kBigLds, "gemm_fp8_big");
+  if (st != kOk) return st;
   // Persistent: one workgroup per CU (the LDS ring allows no more).
-  static int g_cus = 0;
-  if (g_cus <= 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || g_cus <= 0)
-      g_cus = 256;
-  }
-  const int64_t grid = g_cus;
+  const int64_t grid = device_cu_count();
   kern<<<dim3((unsigned)grid), dim3(512), kBigLds, stream>>>(a);
   return launch_status("gemm_fp8_big");
 }

@@ -335,23 +335,10 @@ int launch_w4_prep(const void* x, int64_t ldx, int64_t rows, int64_t H, void* ou
 template <int EPI>
 static int run_w4_tile(const GemmArgs& a, const float* xs, float* xs_out, hipStream_t stream) {
   auto kern = w4_tile_kernel<EPI>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kW4Lds) !=
-        hipSuccess) {
-      set_last_error("w4_tile: cannot reserve %d bytes of LDS", kW4Lds);
-      return kLaunchError;
-    }
-    attr_set = true;
-  }
+  const int st = ensure_dynamic_lds((const void*)kern, kW4Lds, "w4_tile");
+  if (st != kOk) return st;
   // Persistent: one workgroup per CU (the LDS ring allows no more).
-  static int cus = 0;
-  if (cus <= 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-  }
+  const int cus = device_cu_count();
   if (a.m_blocks == 0) return kOk;
   kern<<<dim3((unsigned)cus), dim3(kW4Threads), kW4Lds, stream>>>(a, xs, xs_out);
   return launch_status("w4_tile");

@@ -8,6 +8,16 @@
 
 namespace mstar {
 
+// launch_state.hip: per-device launch state, safe from several host threads.
+// CU count of the current device (cached per device).
+int device_cu_count();
+// Opt `kernel` into `bytes` of dynamic LDS on the current device (once per
+// device and size); kOk or kLaunchError with the message set.
+int ensure_dynamic_lds(const void* kernel, size_t bytes, const char* what);
+// Resident workgroups per CU of `kernel` at this block size and LDS size on
+// the current device (cached per device, kernel, block size and LDS size).
+int occupancy_per_cu(const void* kernel, int threads, size_t lds_bytes);
+
 // route.hip
 // With `hidden` (bf16 [M, H], H % 512 == 0) the launch also quantises the
 // hidden rows per group of 128: hq [M, H] holds the e4m3fn values widened to

@@ -328,15 +328,8 @@ static int run_tile(const GemmArgs& a, hipStream_t stream) {
   using En = Engine<AK, BK>;
   const size_t shmem = (size_t)(BM + BN) * En::kLdr + BM * sizeof(float) + 2 * BM * sizeof(int);
   auto kern = tile_gemm_kernel<AK, BK, EPI, DT, GROUPED, BM, BN>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)shmem) != hipSuccess) {
-      set_last_error("tile_gemm: cannot reserve %zu bytes of LDS", shmem);
-      return kLaunchError;
-    }
-    attr_set = true;
-  }
+  const int st = ensure_dynamic_lds((const void*)kern, shmem, "tile_gemm");
+  if (st != kOk) return st;
   const int n_tiles = (EPI == EPI_ACT) ? (a.inter + BN / 2 - 1) / (BN / 2) : (a.N + BN - 1) / BN;
   const int64_t m_blocks = GROUPED ? a.m_blocks : (a.M + BM - 1) / BM;
   if (m_blocks == 0) return kOk;
@@ -593,15 +586,8 @@ static int run_stream(const GemmArgs& a, hipStream_t stream) {
   constexpr int K = KS * 128;
   const size_t shmem = (size_t)PR * (FP8 ? K + 16 : 2 * K + 16) + (FP8 ? PR * KS * sizeof(float) : 0);
   auto kern = stream_gemm_kernel<BK, EPI, kBF16, KS>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)shmem) != hipSuccess) {
-      set_last_error("stream_gemm: cannot reserve %zu bytes of LDS", shmem);
-      return kLaunchError;
-    }
-    attr_set = true;
-  }
+  const int st = ensure_dynamic_lds((const void*)kern, shmem, "stream_gemm");
+  if (st != kOk) return st;
   const int n_tiles = EPI == EPI_ACT ? (a.inter + 31) / 32 : (a.N + 63) / 64;
   kern<<<dim3(n_tiles, a.num_experts), dim3(256), shmem, stream>>>(a);
   return launch_status("stream_gemm");

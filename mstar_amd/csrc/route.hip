@@ -453,8 +453,8 @@ int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, 
     set_last_error("topk_softmax: invalid arguments (M=%lld E=%d k=%d)", (long long)M, E, k);
     return kInvalidArgument;
   }
-  if (logits_dtype != kF32 && logits_dtype != kBF16) {
-    set_last_error("topk_softmax: logits must be float32 or bfloat16");
+  if (logits_dtype != kF32 && logits_dtype != kBF16 && logits_dtype != kF16) {
+    set_last_error("topk_softmax: logits must be float32, bfloat16 or float16");
     return kUnsupported;
   }
   if (M == 0) return kOk;
@@ -471,6 +471,10 @@ int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, 
       topk_softmax_kernel<float, N><<<grid, block, 0, stream>>>(                             \
           (const float*)logits, M, E, k, renorm, w, ids32, ids64, (const uint16_t*)hidden, H, \
           hq, hs);                                                                           \
+    else if (logits_dtype == kF16)                                                           \
+      topk_softmax_kernel<_Float16, N><<<grid, block, 0, stream>>>(                          \
+          (const _Float16*)logits, M, E, k, renorm, w, ids32, ids64, (const uint16_t*)hidden, \
+          H, hq, hs);                                                                        \
     else                                                                                     \
       topk_softmax_kernel<uint16_t, N><<<grid, block, 0, stream>>>(                          \
           (const uint16_t*)logits, M, E, k, renorm, w, ids32, ids64, (const uint16_t*)hidden, \
@@ -495,15 +499,8 @@ static size_t single_lds(int E) { return sizeof(int) * ((size_t)kAlignWaves * E 
 static size_t scatter_lds(int E) { return sizeof(int) * ((size_t)kAlignWaves * E + 3 * E + 1 + kAlignWaves); }
 
 template <typename K>
-static int opt_in_lds(K kern, size_t bytes, size_t& done) {
-  if (bytes <= 64 * 1024 || bytes <= done) return kOk;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)bytes) != hipSuccess) {
-    set_last_error("routing: cannot reserve %zu bytes of LDS", bytes);
-    return kLaunchError;
-  }
-  done = bytes;
-  return kOk;
+static int opt_in_lds(K kern, size_t bytes) {
+  return ensure_dynamic_lds((const void*)kern, bytes, "routing");
 }
 
 static int check_align_args(const void* ids, int64_t numel, int E, int bm, const int32_t* sorted_ids,
@@ -556,14 +553,13 @@ int launch_align(const void* ids, int ids_dtype, int64_t numel, int E, int bm,
                          scratch_bytes >= align_scratch_bytes(numel, E);
   if (!grid_path) {
     const size_t shmem = single_lds(E);
-    static size_t done32 = 0, done64 = 0;
     if (ids_dtype == kI32) {
-      if ((st = opt_in_lds(align_kernel<int32_t>, shmem, done32)) != kOk) return st;
+      if ((st = opt_in_lds(align_kernel<int32_t>, shmem)) != kOk) return st;
       align_kernel<int32_t><<<1, kAlignThreads, shmem, stream>>>(
           (const int32_t*)ids, numel, E, bm, sorted_ids, expert_ids, ntpp, max_padded, expert_off,
           expert_cnt);
     } else {
-      if ((st = opt_in_lds(align_kernel<int64_t>, shmem, done64)) != kOk) return st;
+      if ((st = opt_in_lds(align_kernel<int64_t>, shmem)) != kOk) return st;
       align_kernel<int64_t><<<1, kAlignThreads, shmem, stream>>>(
           (const int64_t*)ids, numel, E, bm, sorted_ids, expert_ids, ntpp, max_padded, expert_off,
           expert_cnt);
@@ -573,24 +569,21 @@ int launch_align(const void* ids, int ids_dtype, int64_t numel, int E, int bm,
   const int nblocks = (int)((numel + kAlignThreads - 1) / kAlignThreads);
   int32_t* hist = (int32_t*)scratch;
   const size_t hshm = E * sizeof(int), sshm = scatter_lds(E);
-  static size_t d1 = 0, d2 = 0, d3 = 0, d4 = 0;
   if (ids_dtype == kI32) {
     hist_kernel<int32_t><<<nblocks, kAlignThreads, hshm, stream>>>((const int32_t*)ids, numel, E,
                                                                    kAlignThreads, hist);
-    if ((st = opt_in_lds(scatter_kernel<GlobalIds<int32_t>>, sshm, d1)) != kOk) return st;
+    if ((st = opt_in_lds(scatter_kernel<GlobalIds<int32_t>>, sshm)) != kOk) return st;
     scatter_kernel<<<nblocks, kAlignThreads, sshm, stream>>>(
         GlobalIds<int32_t>{(const int32_t*)ids}, numel, E, bm, kAlignThreads, nblocks, hist,
         sorted_ids, expert_ids, ntpp, max_padded, expert_off, expert_cnt);
   } else {
     hist_kernel<int64_t><<<nblocks, kAlignThreads, hshm, stream>>>((const int64_t*)ids, numel, E,
                                                                    kAlignThreads, hist);
-    if ((st = opt_in_lds(scatter_kernel<GlobalIds<int64_t>>, sshm, d2)) != kOk) return st;
+    if ((st = opt_in_lds(scatter_kernel<GlobalIds<int64_t>>, sshm)) != kOk) return st;
     scatter_kernel<<<nblocks, kAlignThreads, sshm, stream>>>(
         GlobalIds<int64_t>{(const int64_t*)ids}, numel, E, bm, kAlignThreads, nblocks, hist,
         sorted_ids, expert_ids, ntpp, max_padded, expert_off, expert_cnt);
   }
-  (void)d3;
-  (void)d4;
   return launch_status("moe_align_block_size");
 }
 
@@ -605,8 +598,7 @@ static int route_impl(const void* logits, int64_t M, int E, int k, int renorm, f
   int st;
   if (numel <= kRouteTopkSmallSlots) {
     const size_t shmem = sizeof(int) * (size_t)((numel + 3) & ~3ll) + single_lds(E);
-    static size_t done = 0;
-    if ((st = opt_in_lds(route_small_kernel<LT, EPL>, shmem, done)) != kOk) return st;
+    if ((st = opt_in_lds(route_small_kernel<LT, EPL>, shmem)) != kOk) return st;
     route_small_kernel<LT, EPL><<<1, kAlignThreads, shmem, stream>>>(
         (const LT*)logits, M, E, k, renorm, w, ids32, ids64, bm, sorted_ids, expert_ids, ntpp,
         max_padded, expert_off, expert_cnt);
@@ -624,8 +616,7 @@ static int route_impl(const void* logits, int64_t M, int E, int k, int renorm, f
   topk_hist_kernel<LT, EPL><<<nblocks, kAlignThreads, E * sizeof(int), stream>>>(
       (const LT*)logits, M, E, k, renorm, w, tmp_ids, ids64, hist, hidden, H, hq, hs, tpb);
   const size_t sshm = scatter_lds(E);
-  static size_t done = 0;
-  if ((st = opt_in_lds(scatter_kernel<GlobalIds<int32_t>>, sshm, done)) != kOk) return st;
+  if ((st = opt_in_lds(scatter_kernel<GlobalIds<int32_t>>, sshm)) != kOk) return st;
   scatter_kernel<<<nblocks, kAlignThreads, sshm, stream>>>(
       GlobalIds<int32_t>{tmp_ids}, numel, E, bm, tpb * k, nblocks, hist,
       sorted_ids, expert_ids, ntpp, max_padded, expert_off, expert_cnt);
@@ -643,8 +634,8 @@ int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, 
   }
   int st = check_align_args(logits, M * k, E, bm, sorted_ids, expert_ids, ntpp, max_padded);
   if (st != kOk) return st;
-  if (logits_dtype != kF32 && logits_dtype != kBF16) {
-    set_last_error("moe_route: logits must be float32 or bfloat16");
+  if (logits_dtype != kF32 && logits_dtype != kBF16 && logits_dtype != kF16) {
+    set_last_error("moe_route: logits must be float32, bfloat16 or float16");
     return kUnsupported;
   }
   if (hidden && (!route_is_grid(M, k) || H <= 0 || H % 128 != 0 || !hq || !hs)) {
@@ -659,6 +650,11 @@ int launch_route(const void* logits, int logits_dtype, int64_t M, int E, int k, 
              ? route_impl<float, N>(logits, M, E, k, renorm, w, ids32, ids64, bm, sorted_ids,   \
                                     expert_ids, ntpp, max_padded, expert_off, expert_cnt,       \
                                     scratch, scratch_bytes, stream, hid, H, hq, hs)             \
+         : logits_dtype == kF16                                                                 \
+             ? route_impl<_Float16, N>(logits, M, E, k, renorm, w, ids32, ids64, bm,            \
+                                       sorted_ids, expert_ids, ntpp, max_padded, expert_off,    \
+                                       expert_cnt, scratch, scratch_bytes, stream, hid, H, hq,  \
+                                       hs)                                                      \
              : route_impl<uint16_t, N>(logits, M, E, k, renorm, w, ids32, ids64, bm,            \
                                        sorted_ids, expert_ids, ntpp, max_padded, expert_off,    \
                                        expert_cnt, scratch, scratch_bytes, stream, hid, H, hq,  \

@@ -982,18 +982,6 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
   wait_vmcnt<0>();  // no DMA outlives the kernel
 }
 
-static int g_num_cu = 0;
-
-static int num_cu() {
-  if (g_num_cu <= 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    g_num_cu = n;
-  }
-  return g_num_cu;
-}
 
 template <int EPI, int KS, bool EXACT, bool AQ>
 static int run_stream_fp8(const GemmArgs& a, hipStream_t stream) {
@@ -1002,24 +990,13 @@ static int run_stream_fp8(const GemmArgs& a, hipStream_t stream) {
                        kStreamRows * 4 + (size_t)a.num_experts * 3 * 4 +
                        (a.topk_ids ? (size_t)a.M * 4 : 0);
   auto kern = stream_fp8_kernel<EPI, KS, EXACT, AQ>;
-  static size_t attr_bytes = 0;  // largest LDS size opted in so far
-  if (shmem > attr_bytes) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)shmem) != hipSuccess) {
-      set_last_error("stream_fp8: cannot reserve %zu bytes of LDS", shmem);
-      return kLaunchError;
-    }
-    attr_bytes = shmem;
-  }
-  // Persistent: as many workgroups as can be resident (at most four per CU).
-  static int occ = 0;
-  if (occ <= 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)kern, 256, shmem) != hipSuccess ||
-        occ <= 0)
-      occ = 1;
-    if (occ > kStreamWgPerCu) occ = kStreamWgPerCu;
-  }
-  const int grid = occ * num_cu();
+  const int st = ensure_dynamic_lds((const void*)kern, shmem, "stream_fp8");
+  if (st != kOk) return st;
+  // Persistent: as many workgroups as can be resident at this LDS size (at
+  // most four per CU).
+  int occ = occupancy_per_cu((const void*)kern, 256, shmem);
+  if (occ > kStreamWgPerCu) occ = kStreamWgPerCu;
+  const int grid = occ * device_cu_count();
   kern<<<dim3(grid), dim3(256), shmem, stream>>>(a);
   return launch_status("stream_fp8");
 }
@@ -1027,16 +1004,9 @@ static int run_stream_fp8(const GemmArgs& a, hipStream_t stream) {
 template <int EPI, int KS, int STAGE>
 static int run_stream_fp8_cu(const GemmArgs& a, int cap, size_t shmem, hipStream_t stream) {
   auto kern = stream_fp8_cu_kernel<EPI, KS, STAGE>;
-  static size_t attr_bytes = 0;
-  if (shmem > attr_bytes) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)shmem) != hipSuccess) {
-      set_last_error("stream_fp8_cu: cannot reserve %zu bytes of LDS", shmem);
-      return kLaunchError;
-    }
-    attr_bytes = shmem;
-  }
-  kern<<<dim3(num_cu()), dim3(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads), shmem, stream>>>(a, cap);
+  const int st = ensure_dynamic_lds((const void*)kern, shmem, "stream_fp8_cu");
+  if (st != kOk) return st;
+  kern<<<dim3(device_cu_count()), dim3(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads), shmem, stream>>>(a, cap);
   return launch_status("stream_fp8_cu");
 }
 

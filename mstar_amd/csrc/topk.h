@@ -15,6 +15,11 @@ template <>
 __device__ inline float load_logit<uint16_t>(const uint16_t* p, int64_t i) {
   return bf16_bits_to_f32(p[i]);
 }
+// fp16 logits (a block run in half precision)
+template <>
+__device__ inline float load_logit<_Float16>(const _Float16* p, int64_t i) {
+  return (float)p[i];
+}
 
 // Order-preserving map fp32 -> uint32 (larger float, larger key).
 __device__ __forceinline__ uint32_t float_key(float v) {

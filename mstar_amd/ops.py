@@ -19,6 +19,24 @@ from ._lib import check, dtype_code, load, ptr, stream_of
 _NS = "mstar_moe"
 
 
+def _on_device(fn):
+    """Run an op with its first tensor argument's device current, as the
+    reference's OptionalCUDAGuard does (moe_align_block_size.cu:213): the
+    launchers size grids and LDS for the current device, and the kernels go
+    to that device's current stream."""
+    import functools
+
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        for a in args:
+            if isinstance(a, torch.Tensor) and a.is_cuda:
+                with torch.cuda.device(a.device):
+                    return fn(*args, **kwargs)
+        return fn(*args, **kwargs)
+
+    return wrapper
+
+
 def _act_code(activation: str) -> int:
     if activation == "silu":
         return 0
@@ -29,6 +47,7 @@ def _act_code(activation: str) -> int:
 
 # ------------------------------------------------------------------ routing
 @torch.library.custom_op(f"{_NS}::topk_softmax", mutates_args=())
+@_on_device
 def topk_softmax(logits: torch.Tensor, top_k: int, renormalize: bool) -> tuple[torch.Tensor, torch.Tensor]:
     _lib.require_gpu(logits)
     logits = logits.contiguous()
@@ -49,6 +68,7 @@ def _(logits, top_k, renormalize):
 
 
 @torch.library.custom_op(f"{_NS}::router", mutates_args=())
+@_on_device
 def router(hidden: torch.Tensor, gate_weight: torch.Tensor, top_k: int,
            renormalize: bool) -> tuple[torch.Tensor, torch.Tensor]:
     """TopKRouter.forward (moe.py:114-140) in one launch: bf16 logits =
@@ -79,6 +99,7 @@ def _(hidden, gate_weight, top_k, renormalize):
 
 
 @torch.library.custom_op(f"{_NS}::moe_align_block_size", mutates_args=())
+@_on_device
 def moe_align_block_size(topk_ids: torch.Tensor, block_size: int,
                          num_experts: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     _lib.require_gpu(topk_ids)
@@ -111,6 +132,7 @@ def _(topk_ids, block_size, num_experts):
 
 
 @torch.library.custom_op(f"{_NS}::moe_route", mutates_args=())
+@_on_device
 def moe_route(logits: torch.Tensor, top_k: int, renormalize: bool, block_size: int
               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """Softmax top-k and alignment in one call: (weights fp32, ids int64,
@@ -152,6 +174,7 @@ def _(logits, top_k, renormalize, block_size):
 
 # --------------------------------------------------------------- elementwise
 @torch.library.custom_op(f"{_NS}::act_and_mul", mutates_args=("out",))
+@_on_device
 def act_and_mul(gate_up: torch.Tensor, out: torch.Tensor, activation: int) -> None:
     _lib.require_gpu(gate_up, out)
     if not (gate_up.is_contiguous() and out.is_contiguous()):
@@ -166,10 +189,13 @@ def act_and_mul(gate_up: torch.Tensor, out: torch.Tensor, activation: int) -> No
 
 
 @torch.library.custom_op(f"{_NS}::moe_sum_reduce", mutates_args=("output",))
+@_on_device
 def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor, routed_scaling_factor: float) -> None:
     _lib.require_gpu(input, output)
     if not (input.is_contiguous() and output.is_contiguous()):
         raise ValueError("moe_sum_reduce: tensors must be contiguous")
+    if input.dtype != output.dtype:
+        raise ValueError(f"moe_sum_reduce: input {input.dtype} and output {output.dtype} dtypes differ")
     T, K, H = input.shape
     if output.shape[0] != T or output.shape[1] != H:
         raise ValueError("moe_sum_reduce: output must be [tokens, hidden]")
@@ -180,13 +206,20 @@ def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor, routed_scaling_fac
 
 # ------------------------------------------------------------ grouped GEMM
 @torch.library.custom_op(f"{_NS}::grouped_gemm", mutates_args=("C",))
+@_on_device
 def grouped_gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
                  topk_weights: Optional[torch.Tensor], sorted_token_ids: torch.Tensor,
                  expert_ids: torch.Tensor, num_tokens_post_padded: torch.Tensor,
                  num_valid_tokens: int, top_k: int, mul_routed_weight: bool,
                  block_size: int) -> None:
     _lib.require_gpu(A, B, C)
+    if not (A.is_contiguous() and B.is_contiguous() and C.is_contiguous()):
+        raise ValueError("grouped_gemm: A, B and C must be contiguous")
+    if A.dtype != B.dtype or A.dtype != C.dtype:
+        raise ValueError("grouped_gemm: A, B and C must share a dtype")
     E, N, K = B.shape
+    if A.shape[-1] != K or C.shape[-1] != N:
+        raise ValueError(f"grouped_gemm: A [.., {A.shape[-1]}] / C [.., {C.shape[-1]}] do not match B {tuple(B.shape)}")
     tw_dt = dtype_code(topk_weights.dtype) if topk_weights is not None else 0
     check(load().mstar_moe_grouped_gemm(
         ptr(A), ptr(B), ptr(C), ptr(topk_weights), tw_dt, ptr(sorted_token_ids), ptr(expert_ids),
@@ -195,12 +228,31 @@ def grouped_gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
 
 
 # ------------------------------------------------------------ fused experts
+def _check_scale(name, s, dtype, shape):
+    if s is None:
+        raise ValueError(f"fused_experts: quantised weights need {name}")
+    if s.dtype != dtype:
+        raise ValueError(f"fused_experts: {name} must be {dtype}, got {s.dtype}")
+    if tuple(s.shape) != tuple(shape):
+        raise ValueError(f"fused_experts: {name} must have shape {tuple(shape)}, got {tuple(s.shape)}")
+    if not s.is_contiguous():
+        raise ValueError(f"fused_experts: {name} must be contiguous")
+
+
 def _check_fused_args(hidden, w1, w2, topk_weights, topk_ids, quant, w1_scale, w2_scale):
     if hidden.dim() != 2:
         raise ValueError("fused_experts: hidden_states must be 2-D [tokens, hidden]")
-    if topk_weights.shape != topk_ids.shape:
-        raise ValueError("fused_experts: topk_weights and topk_ids shapes differ")
+    if topk_weights.shape != topk_ids.shape or topk_ids.dim() != 2:
+        raise ValueError("fused_experts: topk_weights and topk_ids must both be [tokens, top_k]")
+    if w1.dim() != 3 or w2.dim() != 3 or w1.shape[0] != w2.shape[0]:
+        raise ValueError("fused_experts: w1 and w2 must be [E, ., .] with the same E")
+    if not (w1.is_contiguous() and w2.is_contiguous()):
+        raise ValueError("fused_experts: w1 and w2 must be contiguous")
     M, H = hidden.shape
+    if topk_ids.shape[0] != M:
+        raise ValueError(f"fused_experts: topk_ids has {topk_ids.shape[0]} rows for {M} tokens")
+    if topk_ids.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"fused_experts: topk_ids must be int32 or int64, got {topk_ids.dtype}")
     E = w1.shape[0]
     if quant == _lib.QUANT_W4A16:
         two_i, hk = w1.shape[1], w1.shape[2] * 8
@@ -214,12 +266,19 @@ def _check_fused_args(hidden, w1, w2, topk_weights, topk_ids, quant, w1_scale, w
         raise ValueError(f"fused_experts: w2 dim[1] {w2h} != hidden {H}")
     if two_i != 2 * inter:
         raise ValueError(f"fused_experts: w1 dim[1] {two_i} != 2 * w2 inter {2 * inter}")
-    if quant != _lib.QUANT_NONE and (w1_scale is None or w2_scale is None):
-        raise ValueError("fused_experts: quantised weights need w1_scale and w2_scale")
+    if quant == _lib.QUANT_FP8_W8A8:
+        # 128 x 128 weight blocks, fp32 (amax / 448)
+        _check_scale("w1_scale", w1_scale, torch.float32, (E, -(-two_i // 128), H // 128))
+        _check_scale("w2_scale", w2_scale, torch.float32, (E, H // 128, inter // 128))
+    elif quant == _lib.QUANT_W4A16:
+        # one bf16 scale per row and group of 128 along K
+        _check_scale("w1_scale", w1_scale, torch.bfloat16, (E, two_i, H // 128))
+        _check_scale("w2_scale", w2_scale, torch.bfloat16, (E, H, inter // 128))
     return M, H, E, inter
 
 
 @torch.library.custom_op(f"{_NS}::fused_experts", mutates_args=())
+@_on_device
 def fused_experts_op(hidden: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
                      topk_weights: torch.Tensor, topk_ids: torch.Tensor, activation: int,
                      reduce_results: bool, quant: int, w1_scale: Optional[torch.Tensor],
@@ -254,6 +313,7 @@ def _(hidden, w1, w2, topk_weights, topk_ids, activation, reduce_results, quant,
 
 
 @torch.library.custom_op(f"{_NS}::moe_layer", mutates_args=())
+@_on_device
 def moe_layer(hidden: torch.Tensor, router_logits: torch.Tensor, w1: torch.Tensor,
               w2: torch.Tensor, top_k: int, renormalize: bool, activation: int, quant: int,
               w1_scale: Optional[torch.Tensor], w2_scale: Optional[torch.Tensor]
@@ -289,6 +349,7 @@ def _(hidden, router_logits, w1, w2, top_k, renormalize, activation, quant, w1_s
 
 # ---------------------------------------------------------- FP8 quant / GEMM
 @torch.library.custom_op(f"{_NS}::quant_fp8_per_token_group", mutates_args=())
+@_on_device
 def quant_fp8_per_token_group(x: torch.Tensor, group_size: int) -> tuple[torch.Tensor, torch.Tensor]:
     _lib.require_gpu(x)
     x = x.contiguous()
@@ -308,6 +369,7 @@ def _(x, group_size):
 
 
 @torch.library.custom_op(f"{_NS}::quant_fp8_per_token", mutates_args=())
+@_on_device
 def quant_fp8_per_token(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     _lib.require_gpu(x)
     x = x.contiguous()
@@ -326,6 +388,7 @@ def _(x):
 
 
 @torch.library.custom_op(f"{_NS}::fp8_scaled_mm", mutates_args=())
+@_on_device
 def fp8_scaled_mm(a: torch.Tensor, a_scale: torch.Tensor, w: torch.Tensor,
                   w_scale: torch.Tensor) -> torch.Tensor:
     _lib.require_gpu(a, a_scale, w, w_scale)
