@@ -149,7 +149,8 @@ int mstar_moe_sum_reduce(const void* input, void* output, int dtype, int64_t tok
  * Replaces invoke_fused_moe_kernel / fused_moe_kernel
  * (mstar/utils/fused_moe/kernels.py:141-218, 36-138).  block_size must be
  * the one given to mstar_moe_align_block_size (16, 32, 64 or 128);
- * K % 128 == 0.  em = sorted_len. */
+ * any N and K (K and N tails are masked, as kernels.py:97-127 masks them).
+ * em = sorted_len. */
 int mstar_moe_grouped_gemm(const void* A, const void* B, void* C, const void* topk_weights,
                            int topk_w_dtype, const int32_t* sorted_token_ids,
                            const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
@@ -172,7 +173,8 @@ int mstar_moe_grouped_gemm(const void* A, const void* B, void* C, const void* to
  *   from mstar_moe_align_block_size with this block_size), 2 = weight
  *   streaming (needs expert_offsets/expert_counts; 16-bit A, quantised B;
  *   FP8 activations are quantised per 128-group on the fly).
- * The A row of a slot is slot / top_k. */
+ * The A row of a slot is slot / top_k.  Quantised B needs K % 128 == 0; quant
+ * NONE takes any K. */
 int mstar_moe_gemm(const void* A, int a_dtype, const float* a_scale, const void* B, int quant,
                    const void* b_scale, void* C, int c_dtype, const void* topk_weights,
                    int topk_w_dtype, const int32_t* sorted_token_ids, const int32_t* expert_ids,
@@ -220,7 +222,8 @@ int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_e
  *   topk_weights [num_tokens, top_k] fp32/bf16/fp16; topk_ids int32/int64;
  *   out [num_tokens, hidden_size], or [num_tokens, top_k, hidden_size] when
  *   reduce_results == 0 (runner.py:155-156).
- * hidden_size and inter must be multiples of 128. */
+ * Quantised paths: hidden_size and inter must be multiples of 128; the
+ * bf16/fp16 path takes any sizes. */
 int mstar_fused_moe(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
                     const void* w1, const void* w2, int num_experts, int64_t inter, int quant,
                     const void* w1_scale, const void* w2_scale, const void* topk_weights,

@@ -83,9 +83,9 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
                    (long long)M, (long long)H, E, (long long)I, top_k);
     return kInvalidArgument;
   }
-  if (H % 128 != 0 || I % 128 != 0) {
-    set_last_error("fused_moe: hidden and intermediate sizes must be multiples of 128 "
-                   "(H=%lld I=%lld)", (long long)H, (long long)I);
+  if (quant != MSTAR_QUANT_NONE && (H % 128 != 0 || I % 128 != 0)) {
+    set_last_error("fused_moe: quantised paths need hidden and intermediate sizes that are "
+                   "multiples of 128 (H=%lld I=%lld)", (long long)H, (long long)I);
     return kUnsupported;
   }
   if (quant != MSTAR_QUANT_NONE && act_dtype != kBF16) {
@@ -454,7 +454,7 @@ int mstar_moe_gemm(const void* A, int a_dtype, const float* a_scale, const void*
                    const int32_t* expert_counts, int num_experts, int64_t N, int64_t K,
                    int64_t em, int64_t num_valid_tokens, int top_k, int mul_routed_weight,
                    int activation, int block_size, int path, void* stream) {
-  if (N <= 0 || K <= 0 || K % 128 != 0 || num_experts <= 0 || top_k <= 0 || !A || !B || !C ||
+  if (N <= 0 || K <= 0 || (quant != MSTAR_QUANT_NONE && K % 128 != 0) || num_experts <= 0 || top_k <= 0 || !A || !B || !C ||
       !sorted_token_ids || (mul_routed_weight && !topk_weights) ||
       (quant != MSTAR_QUANT_NONE && !b_scale) || activation < -1 || activation > 1 ||
       (activation >= 0 && N % 2 != 0) || path < 0 || path > 2) {

@@ -5,7 +5,8 @@
 //    with gate = columns [0, I), up = columns [I, 2I).
 //  * sum_reduce_kernel restates moe_sum_reduce_kernel (kernels.py:306-356):
 //    fp32 sum over the top-k dimension, times the scaling factor, cast.
-// Both move 16 bytes per lane per access.
+// Both move 16 bytes per lane per access; sizes that are not a multiple of
+// 8 elements take one-element-per-thread variants.
 #include "common.h"
 #include "launch.h"
 
@@ -83,14 +84,59 @@ __global__ __launch_bounds__(256) void sum_reduce_kernel(const uint16_t* __restr
   *(v4i*)(out + t * hidden + c) = o;
 }
 
+// One element per thread: sizes that are not a multiple of 8 elements, or
+// rows not 16-byte aligned.  Same arithmetic as the vector kernels.
+template <int DT, int ACT>
+__global__ __launch_bounds__(256) void act_and_mul_scalar_kernel(const uint16_t* __restrict__ gu,
+                                                                 uint16_t* __restrict__ out,
+                                                                 int64_t rows, int64_t inter) {
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (v >= rows * inter) return;
+  const int64_t r = v / inter, c = v % inter;
+  const float g = h16_to_f32<DT>(gu[r * 2 * inter + c]);
+  const float u = h16_to_f32<DT>(gu[r * 2 * inter + inter + c]);
+  out[v] = f32_to_h16<DT>(round_h16<DT>(act_f32<ACT>(g)) * u);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void sum_reduce_scalar_kernel(const uint16_t* __restrict__ in,
+                                                                uint16_t* __restrict__ out,
+                                                                int64_t tokens, int topk,
+                                                                int64_t hidden, float scale) {
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (v >= tokens * hidden) return;
+  const int64_t t = v / hidden, c = v % hidden;
+  float acc = 0.f;
+  for (int j = 0; j < topk; ++j) acc += h16_to_f32<DT>(in[(t * topk + j) * hidden + c]);
+  out[v] = f32_to_h16<DT>(acc * scale);
+}
+
+static bool aligned16(const void* a, const void* b) {
+  return (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
+}
+
 int launch_act_and_mul(const void* gate_up, void* out, int dtype, int64_t rows, int64_t inter,
                        int activation, hipStream_t stream) {
-  if (rows < 0 || inter <= 0 || inter % 8 != 0 || (activation != 0 && activation != 1)) {
-    set_last_error("act_and_mul: inter must be a positive multiple of 8 (inter=%lld)",
+  if (rows < 0 || inter <= 0 || (activation != 0 && activation != 1)) {
+    set_last_error("act_and_mul: inter must be positive and activation 0 or 1 (inter=%lld)",
                    (long long)inter);
     return kInvalidArgument;
   }
   if (rows == 0) return kOk;
+  if (inter % 8 != 0 || !aligned16(gate_up, out)) {
+    dim3 g1((unsigned)((rows * inter + 255) / 256));
+    const uint16_t* gu = (const uint16_t*)gate_up;
+    uint16_t* o = (uint16_t*)out;
+    if (dtype == kBF16 && activation == 0) act_and_mul_scalar_kernel<kBF16, 0><<<g1, 256, 0, stream>>>(gu, o, rows, inter);
+    else if (dtype == kBF16) act_and_mul_scalar_kernel<kBF16, 1><<<g1, 256, 0, stream>>>(gu, o, rows, inter);
+    else if (dtype == kF16 && activation == 0) act_and_mul_scalar_kernel<kF16, 0><<<g1, 256, 0, stream>>>(gu, o, rows, inter);
+    else if (dtype == kF16) act_and_mul_scalar_kernel<kF16, 1><<<g1, 256, 0, stream>>>(gu, o, rows, inter);
+    else {
+      set_last_error("act_and_mul: dtype must be bf16 or fp16");
+      return kUnsupported;
+    }
+    return launch_status("act_and_mul");
+  }
   dim3 grid((unsigned)((rows * (inter / 8) + 255) / 256));
   const uint16_t* gu = (const uint16_t*)gate_up;
   uint16_t* o = (uint16_t*)out;
@@ -107,12 +153,26 @@ int launch_act_and_mul(const void* gate_up, void* out, int dtype, int64_t rows, 
 
 int launch_sum_reduce(const void* in, void* out, int dtype, int64_t tokens, int64_t topk,
                       int64_t hidden, float scale, hipStream_t stream) {
-  if (tokens < 0 || topk <= 0 || hidden <= 0 || hidden % 8 != 0) {
-    set_last_error("moe_sum_reduce: hidden must be a positive multiple of 8 (hidden=%lld)",
-                   (long long)hidden);
+  if (tokens < 0 || topk <= 0 || topk > INT32_MAX || hidden <= 0) {
+    set_last_error("moe_sum_reduce: invalid sizes (tokens=%lld top_k=%lld hidden=%lld)",
+                   (long long)tokens, (long long)topk, (long long)hidden);
     return kInvalidArgument;
   }
   if (tokens == 0) return kOk;
+  if (hidden % 8 != 0 || !aligned16(in, out)) {
+    dim3 g1((unsigned)((tokens * hidden + 255) / 256));
+    if (dtype == kBF16)
+      sum_reduce_scalar_kernel<kBF16><<<g1, 256, 0, stream>>>((const uint16_t*)in, (uint16_t*)out, tokens,
+                                                               (int)topk, hidden, scale);
+    else if (dtype == kF16)
+      sum_reduce_scalar_kernel<kF16><<<g1, 256, 0, stream>>>((const uint16_t*)in, (uint16_t*)out, tokens,
+                                                              (int)topk, hidden, scale);
+    else {
+      set_last_error("moe_sum_reduce: dtype must be bf16 or fp16");
+      return kUnsupported;
+    }
+    return launch_status("moe_sum_reduce");
+  }
   dim3 grid((unsigned)((tokens * (hidden / 8) + 255) / 256));
   if (dtype == kBF16)
     sum_reduce_kernel<kBF16, false><<<grid, 256, 0, stream>>>((const uint16_t*)in, nullptr, (uint16_t*)out, tokens,

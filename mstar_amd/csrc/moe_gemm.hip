@@ -188,10 +188,40 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs p) {
     if (tid < BM && sRow[tid] >= 0) as_ptr = p.a_scale + (int64_t)sRow[tid] * p.ld_as;
   }
 
+  // 16-bit operands take any K: the last 128-K step (and every step when a
+  // row is not 16-byte aligned) loads element by element and zero-fills the
+  // columns at or past K, so both operands contribute exact zeros there.
+  constexpr bool KTAIL = AK == A_H16 && BK == B_H16;
+  bool vec_ok = true;
+  if constexpr (KTAIL)
+    vec_ok = ((p.lda | p.ldb | p.b_estride) & 7) == 0 && (((uintptr_t)p.A | (uintptr_t)p.B) & 15) == 0;
+  auto load_h16_chunk = [&](const uint8_t* ptr, int col, int kb) -> v4i {
+    v4i r = {0, 0, 0, 0};
+    if (!ptr) return r;
+    const uint16_t* e = (const uint16_t*)(ptr + (int64_t)kb * RB);
+    const int k0 = kb * 128 + col * 8;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const uint32_t lo = k0 + 2 * n < p.K ? e[2 * n] : 0u;
+      const uint32_t hi = k0 + 2 * n + 1 < p.K ? e[2 * n + 1] : 0u;
+      r[n] = (int)(lo | (hi << 16));
+    }
+    return r;
+  };
+
   v4i ra[CA], rb[CB];
   float ras = 0.f;
   float rbs[CB];
   auto load_step = [&](int kb) {
+    if constexpr (KTAIL) {
+      if (!vec_ok || (kb + 1) * 128 > p.K) {
+#pragma unroll
+        for (int i = 0; i < CA; ++i) ra[i] = load_h16_chunk(a_ptr[i], a_col[i], kb);
+#pragma unroll
+        for (int i = 0; i < CB; ++i) rb[i] = load_h16_chunk(b_ptr[i], b_col[i], kb);
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < CA; ++i)
       ra[i] = a_ptr[i] ? *(const v4i*)(a_ptr[i] + (int64_t)kb * RB) : v4i{0, 0, 0, 0};
@@ -230,7 +260,7 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const int KB = p.K / 128;
+  const int KB = KTAIL ? (p.K + 127) / 128 : p.K / 128;
   load_step(0);
   for (int kb = 0; kb < KB; ++kb) {
     store_step();
@@ -358,8 +388,10 @@ static int dispatch_bm(const GemmArgs& a, int bm, hipStream_t s) {
 
 int launch_tile_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dtype, bool grouped,
                      int bm, hipStream_t stream) {
-  if (a.K <= 0 || a.K % 128 != 0 || a.N <= 0 || (epi == EPI_ACT && a.N != 2 * a.inter)) {
-    set_last_error("tile_gemm: K must be a positive multiple of 128 (K=%d, N=%d)", a.K, a.N);
+  const bool any_k = akind == A_H16 && bkind == B_H16;
+  if (a.K <= 0 || (!any_k && a.K % 128 != 0) || a.N <= 0 || (epi == EPI_ACT && a.N != 2 * a.inter)) {
+    set_last_error("tile_gemm: K must be positive (a multiple of 128 for quantised operands; "
+                   "K=%d, N=%d)", a.K, a.N);
     return kInvalidArgument;
   }
   if (grouped && (!a.sorted_ids || !a.expert_ids || !a.ntpp)) {
