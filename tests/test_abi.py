@@ -72,9 +72,13 @@ def test_fused_moe_workspace_and_shape_checks():
     assert lib.mstar_fused_moe_workspace_size(32, 2048, 128, 768, 8, _lib.QUANT_FP8_W8A8,
                                               _lib.DT_BF16, 1, ctypes.byref(n)) == 0
     assert n.value > 32 * 8 * 768 * 2
-    assert lib.mstar_fused_moe_workspace_size(32, 2000, 128, 768, 8, 0, _lib.DT_BF16, 1,
-                                              ctypes.byref(n)) == 2
+    # quantised paths need multiples of 128; the bf16 path takes any size
+    assert lib.mstar_fused_moe_workspace_size(32, 2000, 128, 768, 8, _lib.QUANT_FP8_W8A8,
+                                              _lib.DT_BF16, 1, ctypes.byref(n)) == 2
     assert "multiples of 128" in _err()
+    assert lib.mstar_fused_moe_workspace_size(32, 2000, 128, 100, 8, 0, _lib.DT_BF16, 1,
+                                              ctypes.byref(n)) == 0
+    assert n.value >= 32 * 8 * 100 * 2 + 32 * 8 * 2000 * 2
     assert lib.mstar_fused_moe_workspace_size(32, 2048, 128, 768, 200, 0, _lib.DT_BF16, 1,
                                               ctypes.byref(n)) == 1
     # fp16 activations are not accepted by the quantised paths
