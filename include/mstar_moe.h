@@ -252,6 +252,25 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
                     void* out, float* topk_weights_out, int64_t* topk_ids_out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* mstar_moe_layer without a workspace argument: it allocates nothing
+ * (no hipMalloc/hipFree, no allocating library call).  No counterpart in
+ * the reference; it is for callers that cannot allocate (code under stream
+ * capture, serving loops and harnesses that forbid hipMalloc).  The
+ * workspace is a fixed device array of MSTAR_MOE_NOALLOC_SCRATCH_BYTES held
+ * by the library on each device until the process ends; sizes whose
+ * mstar_moe_layer_workspace_size exceeds it return
+ * MSTAR_WORKSPACE_TOO_SMALL (16 MiB covers, e.g., 256 tokens of a 2048 /
+ * 128 x 768 / top-8 layer in every quant mode).  All calls on one device
+ * share that array: calls that overlap in time on one device (two streams
+ * or two threads) race.  Arguments and results as mstar_moe_layer. */
+#define MSTAR_MOE_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int mstar_moe_layer_noalloc(const void* hidden, int act_dtype, int64_t num_tokens,
+                            int64_t hidden_size, const void* router_logits, int logits_dtype,
+                            int renormalize, const void* w1, const void* w2, int num_experts,
+                            int64_t inter, int quant, const void* w1_scale, const void* w2_scale,
+                            int top_k, int activation, void* out, float* topk_weights_out,
+                            int64_t* topk_ids_out, void* stream);
+
 /* Activation quantisation, OCP e4m3fn: per token-group of 128
  * (s = max(amax, 1e-10) / 448, scales [rows, cols/128]) or per token
  * (scales [rows]).  No reference counterpart: the reference's FP8 branches

@@ -74,6 +74,9 @@ SIGNATURES = {
     "mstar_moe_layer": (
         _c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _c_int, _vp, _vp, _c_int, _c_i64, _c_int,
                  _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "mstar_moe_layer_noalloc": (
+        _c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _c_int, _vp, _vp, _c_int, _c_i64, _c_int,
+                 _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp]),
     "mstar_quant_fp8_per_token_group": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_int, _vp, _vp, _vp]),
     "mstar_quant_fp8_per_token": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mstar_fp8_scaled_mm": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
