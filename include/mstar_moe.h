@@ -252,6 +252,22 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
                     void* out, float* topk_weights_out, int64_t* topk_ids_out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* The routed layer from the hidden states: the fused router
+ * (mstar_moe_router: gate projection x . gate_weight^T in bf16, softmax,
+ * top-k, renormalisation) -> align -> gate_up GEMM (+ activation) -> down
+ * GEMM (x routed weight) -> top-k sum, as one call.  Replaces the routed half
+ * of SparseMoeBlock.forward whole (mstar/model/components/moe.py:245-261,
+ * TopKRouter.forward moe.py:130-140 included).  bf16 hidden and gate_weight
+ * [num_experts, hidden_size] (num_experts <= 256, hidden_size % 32 == 0);
+ * workspace from mstar_moe_layer_workspace_size; logits_out [num_tokens,
+ * num_experts] bf16, topk_weights_out and topk_ids_out are optional. */
+int mstar_moe_block(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                    const void* gate_weight, int renormalize, const void* w1, const void* w2,
+                    int num_experts, int64_t inter, int quant, const void* w1_scale,
+                    const void* w2_scale, int top_k, int activation, void* out,
+                    float* topk_weights_out, int64_t* topk_ids_out, void* logits_out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* mstar_moe_layer without a workspace argument: it allocates nothing
  * (no hipMalloc/hipFree, no allocating library call).  No counterpart in
  * the reference; it is for callers that cannot allocate (code under stream

@@ -74,6 +74,9 @@ SIGNATURES = {
     "mstar_moe_layer": (
         _c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _c_int, _vp, _vp, _c_int, _c_i64, _c_int,
                  _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "mstar_moe_block": (
+        _c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _vp, _vp, _c_int, _c_i64, _c_int,
+                 _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "mstar_moe_layer_noalloc": (
         _c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _c_int, _vp, _vp, _c_int, _c_i64, _c_int,
                  _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp]),

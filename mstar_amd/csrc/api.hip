@@ -606,6 +606,49 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
                      ws, stream);
 }
 
+int mstar_moe_block(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                    const void* gate_weight, int renormalize, const void* w1, const void* w2,
+                    int num_experts, int64_t inter, int quant, const void* w1_scale,
+                    const void* w2_scale, int top_k, int activation, void* out,
+                    float* topk_weights_out, int64_t* topk_ids_out, void* logits_out,
+                    void* workspace, size_t workspace_bytes, void* stream_) {
+  hipStream_t stream = (hipStream_t)stream_;
+  if (act_dtype != kBF16) {
+    set_last_error("moe_block: the fused router takes bf16 hidden states and gate weight");
+    return kUnsupported;
+  }
+  Plan pl;
+  int st = make_plan(num_tokens, hidden_size, num_experts, inter, top_k, quant, act_dtype, 1, &pl,
+                     true);
+  if (st != kOk) return st;
+  // The router launch does not quantise the hidden rows: the experts read
+  // (and, where needed, quantise) them as mstar_fused_moe does.
+  pl.route_quant = false;
+  if ((st = check_layer_args(pl, activation, workspace, workspace_bytes)) != kOk) return st;
+  if (num_tokens == 0) return kOk;
+  if (!hidden || !gate_weight || !w1 || !w2 || !out ||
+      (quant != MSTAR_QUANT_NONE && (!w1_scale || !w2_scale))) {
+    set_last_error("moe_block: null tensor pointer");
+    return kInvalidArgument;
+  }
+  uint8_t* ws = (uint8_t*)workspace;
+  float* tw = topk_weights_out ? topk_weights_out : (float*)(ws + pl.off_tw);
+  int32_t* ids32 = (int32_t*)(ws + pl.off_ids);
+  st = launch_router(hidden, num_tokens, hidden_size, gate_weight, num_experts, top_k, renormalize,
+                     tw, ids32, topk_ids_out, logits_out, stream);
+  if (st != kOk) return st;
+  if (!pl.ids_mode) {
+    st = launch_align(ids32, kI32, pl.slots, num_experts, pl.bm, (int32_t*)(ws + pl.off_sorted),
+                      (int32_t*)(ws + pl.off_eids), (int32_t*)(ws + pl.off_ntpp), pl.max_padded,
+                      (int32_t*)(ws + pl.off_eoff), (int32_t*)(ws + pl.off_ecnt),
+                      ws + pl.off_scratch, pl.scratch_bytes, stream);
+    if (st != kOk) return st;
+  }
+  return run_experts(pl, hidden, act_dtype, num_tokens, hidden_size, w1, w2, num_experts, inter,
+                     quant, w1_scale, w2_scale, tw, kF32, ids32, kI32, top_k, activation, 1, out,
+                     ws, stream);
+}
+
 int mstar_moe_route(const void* router_logits, int logits_dtype, int64_t num_tokens,
                     int num_experts, int top_k, int renormalize, float* topk_weights,
                     int32_t* topk_ids_i32, int64_t* topk_ids_i64, int block_size,

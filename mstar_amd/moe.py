@@ -32,10 +32,15 @@ class TopKRouter(nn.Module):
         self.norm_topk_prob = norm_topk_prob
         self.weight = nn.Parameter(torch.zeros(num_experts, hidden_size))
 
+    def fused_ok(self, hidden_states: torch.Tensor) -> bool:
+        """Whether the fused router kernel takes these states (bf16 states
+        and weight, at most 256 experts, hidden size a multiple of 32)."""
+        return (hidden_states.dtype == torch.bfloat16 and self.weight.dtype == torch.bfloat16
+                and self.num_experts <= 256 and hidden_states.shape[-1] % 32 == 0)
+
     def forward(self, hidden_states: torch.Tensor, router_states: torch.Tensor | None = None):
         hidden_states = hidden_states.reshape(-1, hidden_states.shape[-1])
-        if (hidden_states.dtype == torch.bfloat16 and self.weight.dtype == torch.bfloat16
-                and self.num_experts <= 256 and hidden_states.shape[-1] % 32 == 0):
+        if self.fused_ok(hidden_states):
             w, ids = ops.router(hidden_states, self.weight, self.top_k, self.norm_topk_prob)
             return w, ids, None
         router_logits = F.linear(hidden_states, self.weight)
@@ -103,12 +108,18 @@ class SparseMoeBlock(nn.Module):
 
     def routed(self, flat, router_states=None):
         """Routed experts of ``flat [T, H]`` -> ``(out, router_states_next)``.
-        With the default router the gate projection stays an ``F.linear``
-        and everything after it (softmax top-k, align, both GEMMs, the
-        top-k sum) is one library call."""
+        With the default router the whole routed layer -- gate projection,
+        softmax top-k, align, both GEMMs, the top-k sum -- is one library
+        call (the fused router for bf16 states, as TopKRouter uses it; for
+        other dtypes the gate projection is an ``F.linear`` first)."""
         if type(self.gate) is TopKRouter:
-            logits = F.linear(flat, self.gate.weight)
             ex = self.experts
+            if self.gate.fused_ok(flat):
+                out, _, _ = ops.moe_block(flat, self.gate.weight, ex.gate_up_proj, ex.down_proj,
+                                          self.gate.top_k, self.gate.norm_topk_prob, 0,
+                                          _quant_code(ex.quant), ex.w1_scale, ex.w2_scale)
+                return out, None
+            logits = F.linear(flat, self.gate.weight)
             out, _, _ = ops.moe_layer(flat, logits, ex.gate_up_proj, ex.down_proj, self.gate.top_k,
                                       self.gate.norm_topk_prob, 0, _quant_code(ex.quant),
                                       ex.w1_scale, ex.w2_scale)

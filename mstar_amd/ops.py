@@ -347,6 +347,44 @@ def _(hidden, router_logits, w1, w2, top_k, renormalize, activation, quant, w1_s
             hidden.new_empty(M, top_k, dtype=torch.int64))
 
 
+@torch.library.custom_op(f"{_NS}::moe_block", mutates_args=())
+@_on_device
+def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, w1: torch.Tensor,
+              w2: torch.Tensor, top_k: int, renormalize: bool, activation: int, quant: int,
+              w1_scale: Optional[torch.Tensor], w2_scale: Optional[torch.Tensor]
+              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Routed MoE layer from the hidden states (fused router + experts, one
+    library call): (out, topk_weights fp32, topk_ids int64)."""
+    _lib.require_gpu(hidden, gate_weight, w1, w2)
+    if hidden.dtype != torch.bfloat16 or gate_weight.dtype != torch.bfloat16:
+        raise ValueError("moe_block: hidden states and gate weight must be bfloat16")
+    dummy_ids = torch.empty(hidden.shape[0], top_k, dtype=torch.int64, device=hidden.device)
+    dummy_w = torch.empty(hidden.shape[0], top_k, dtype=torch.float32, device=hidden.device)
+    M, H, E, inter = _check_fused_args(hidden, w1, w2, dummy_w, dummy_ids, quant, w1_scale, w2_scale)
+    gate_weight = gate_weight.contiguous()
+    if tuple(gate_weight.shape) != (E, H):
+        raise ValueError(f"moe_block: gate weight must be [{E}, {H}], got {tuple(gate_weight.shape)}")
+    lib = load()
+    act_dt = dtype_code(hidden.dtype)
+    nbytes = ctypes.c_size_t(0)
+    check(lib.mstar_moe_layer_workspace_size(M, H, E, inter, top_k, quant, act_dt,
+                                             ctypes.byref(nbytes)), "moe_block")
+    ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=hidden.device)
+    out = torch.empty(M, H, dtype=hidden.dtype, device=hidden.device)
+    check(lib.mstar_moe_block(
+        ptr(hidden), act_dt, M, H, ptr(gate_weight), int(renormalize), ptr(w1), ptr(w2), E, inter,
+        quant, ptr(w1_scale), ptr(w2_scale), top_k, activation, ptr(out), ptr(dummy_w),
+        ptr(dummy_ids), None, ptr(ws), nbytes.value, stream_of(hidden)), "moe_block")
+    return out, dummy_w, dummy_ids
+
+
+@moe_block.register_fake
+def _(hidden, gate_weight, w1, w2, top_k, renormalize, activation, quant, w1_scale, w2_scale):
+    M, H = hidden.shape
+    return (hidden.new_empty(M, H), hidden.new_empty(M, top_k, dtype=torch.float32),
+            hidden.new_empty(M, top_k, dtype=torch.int64))
+
+
 # ---------------------------------------------------------- FP8 quant / GEMM
 @torch.library.custom_op(f"{_NS}::quant_fp8_per_token_group", mutates_args=())
 @_on_device

@@ -180,7 +180,8 @@ def _fp8_ref(x, q1, s1, q2, s2, tw, ti):
     return O.fused_experts_rounding(x, None, None, tw, ti, w1_dq=d1, w2_dq=d2, act_quant=True)
 
 
-@pytest.mark.parametrize("M,bias", [(32, False), (1, False), (64, True), (512, True), (2048, False)])
+@pytest.mark.parametrize("M,bias", [(32, False), (1, False), (64, True), (512, True), (2048, True),
+                                    (2048, False)])
 def test_fused_experts_fp8_thinker(M, bias):
     """Config 2 (decode, M=32; weight-streaming path for M <= 64) and config 3
     (prefill with the Zipf bias; tiled path) at Qwen3-30B-A3B thinker shapes."""
@@ -193,6 +194,30 @@ def test_fused_experts_fp8_thinker(M, bias):
                         w1_scale=s1, w2_scale=s2, block_shape=(128, 128))
     ref = _fp8_ref(x, q1, s1, q2, s2, tw, ti)
     assert_moe_close(out, ref, what=f"fp8 M={M}")
+
+
+def test_moe_layer_prefill_8192_zipf_rows():
+    """Config 3's headline point: 8192 tokens, Zipf-biased routing (expert 0
+    takes thousands of slots), the whole layer from logits.  Each token's
+    output depends on its own row only (its activation quantisation is per
+    token and group), so the oracle scores 320 fixed rows: the first 128,
+    128 routed to expert 0 and 64 spread over the batch."""
+    from mstar_amd import _lib, ops
+    M, H, E, I, k = 8192, 2048, 128, 768, 8
+    q1, s1, q2, s2 = _fp8_weights(H, E, I)
+    x = _hidden(M, H, seed=8192)
+    g = torch.Generator().manual_seed(8193)
+    logits = torch.randn(M, E, generator=g) + O.zipf_bias(E)
+    rw, rids = O.router_topk_softmax(logits, k, True)
+    out, tw, ti = ops.moe_layer(x.to(DEV), logits.to(DEV), q1, q2, k, True, 0, _lib.QUANT_FP8_W8A8,
+                                s1, s2)
+    assert torch.equal(ti.cpu(), rids)
+    to_e0 = torch.nonzero((rids == 0).any(dim=1)).flatten()
+    assert to_e0.numel() > 1000  # the skew the bench times
+    rows = torch.cat([torch.arange(128), to_e0[torch.randperm(to_e0.numel(), generator=g)[:128]],
+                      torch.randint(0, M, (64,), generator=g)]).unique()
+    ref = _fp8_ref(x[rows], q1, s1, q2, s2, rw[rows], rids[rows])
+    assert_moe_close(out.cpu()[rows], ref, what="moe_layer fp8 M=8192 zipf rows")
 
 
 @pytest.mark.parametrize("reduce", [True, False])
