@@ -12,6 +12,10 @@
   (``experts.gate_up_proj [E, 2I, H]`` rows ``[gate; up]``,
   ``experts.down_proj [E, H, I]``) plus :meth:`quantize` to switch the
   experts to FP8 (block 128x128) or W4A16 (group 128) storage.
+* :class:`ParallelSparseMoeBlock` / :class:`ParallelSparseMoeBlockWithSharedExpert`
+  -- the tensor-parallel blocks (moe.py:378-591): experts sharded along the
+  intermediate size, per-expert weight loaders, the routed output summed
+  over the group (RCCL through ``torch.distributed``).
 """
 from __future__ import annotations
 
@@ -153,3 +157,133 @@ class SparseMoeBlockWithSharedExpert(SparseMoeBlock):
         routed, router_states_next = self.routed(flat, router_states)
         out = (routed + torch.sigmoid(self.shared_expert_gate(flat)) * shared).view(input_shape)
         return (out, router_states_next) if return_router_states else out
+
+
+# ---------------------------------------------------------------------------
+# Tensor-parallel blocks (moe.py:378-591): experts sharded along the
+# intermediate dimension, the routed output summed over the group.
+# ---------------------------------------------------------------------------
+class ProcessGroupComm:
+    """The communication-group interface the blocks use (``rank``,
+    ``world_size``, in-place sum ``all_reduce``; the reference's
+    ``CommGroup``, mstar/distributed/communication.py:8-36, fits it as is)
+    over a ``torch.distributed`` group.  On ROCm the ``nccl`` backend is
+    RCCL and reduces device tensors directly; a ``gloo`` group is handed a
+    synchronous host copy (gloo collectives take CPU tensors)."""
+
+    def __init__(self, group=None) -> None:
+        import torch.distributed as dist
+        self.group = group
+        self.rank = dist.get_rank(group)
+        self.world_size = dist.get_world_size(group)
+
+    @classmethod
+    def trivial(cls) -> "ProcessGroupComm":
+        c = cls.__new__(cls)
+        c.group, c.rank, c.world_size = None, 0, 1
+        return c
+
+    def all_reduce(self, t: torch.Tensor) -> torch.Tensor:
+        if self.world_size == 1:
+            return t
+        import torch.distributed as dist
+        if t.is_cuda and dist.get_backend(self.group) == "gloo":
+            h = t.cpu()
+            dist.all_reduce(h, group=self.group)
+            t.copy_(h)
+        else:
+            dist.all_reduce(t, group=self.group)
+        return t
+
+
+def _divide(n: int, d: int) -> int:
+    if n % d:
+        raise ValueError(f"{n} is not divisible by {d}")
+    return n // d
+
+
+@torch.no_grad()
+def gate_up_weight_loader(tp_rank: int, tp_size: int, full_inter: int, param: nn.Parameter,
+                          loaded_weight: torch.Tensor, loaded_shard_id: str) -> None:
+    """One expert's ``gate_proj`` / ``up_proj`` ``[inter, hidden]``
+    (``loaded_shard_id`` ``"gate:N"`` / ``"up:N"``) into rank ``tp_rank``'s
+    ``gate_up_proj [E, 2 I/P, H]``: its row slice, gate rows first
+    (moe.py:335-359)."""
+    kind, expert = loaded_shard_id.split(":")
+    shard = _divide(full_inter, tp_size)
+    rows = loaded_weight[tp_rank * shard:(tp_rank + 1) * shard, :]
+    if kind not in ("gate", "up"):
+        raise ValueError(f"unknown shard id {loaded_shard_id!r}")
+    off = 0 if kind == "gate" else shard
+    param.data[int(expert), off:off + shard, :] = rows
+
+
+@torch.no_grad()
+def down_proj_weight_loader(tp_rank: int, tp_size: int, full_inter: int, param: nn.Parameter,
+                            loaded_weight: torch.Tensor, loaded_shard_id: str) -> None:
+    """One expert's ``down_proj`` ``[hidden, inter]`` (``"down:N"``) into
+    rank ``tp_rank``'s ``down_proj [E, H, I/P]``: its column slice
+    (moe.py:362-375)."""
+    shard = _divide(full_inter, tp_size)
+    param.data[int(loaded_shard_id.split(":")[1])] = loaded_weight[:, tp_rank * shard:(tp_rank + 1) * shard]
+
+
+class _TensorParallel:
+    """Shared by the two tensor-parallel blocks: the rank's expert shard, its
+    weight loaders, and the group sum of the routed output."""
+
+    def _init_tp(self, comm_group, full_inter: int) -> int:
+        self.comm_group = comm_group if comm_group is not None else ProcessGroupComm.trivial()
+        return _divide(full_inter, self.comm_group.world_size)
+
+    def _attach_weight_loaders(self) -> None:
+        from functools import partial
+        r, p, full = self.comm_group.rank, self.comm_group.world_size, self.moe_intermediate_size
+        self.experts.gate_up_proj.weight_loader = partial(gate_up_weight_loader, r, p, full)
+        self.experts.down_proj.weight_loader = partial(down_proj_weight_loader, r, p, full)
+
+    def _apply(self, fn, recurse=True):
+        result = super()._apply(fn, recurse=recurse)
+        if hasattr(self, "comm_group"):
+            self._attach_weight_loaders()
+        return result
+
+    def routed(self, flat, router_states=None):
+        """The rank's partial routed output (its shard of every expert,
+        top-k sum included), then the sum over the group.  The reference
+        (``_dispatch_tp``, moe.py:467-482) sums the top-k in fp32 and
+        stores bf16 before its all-reduce; the fused layer does the same."""
+        out, router_states_next = super().routed(flat, router_states)
+        self.comm_group.all_reduce(out)
+        return out, router_states_next
+
+
+class ParallelSparseMoeBlock(_TensorParallel, SparseMoeBlock):
+    """Tensor-parallel ``SparseMoeBlock`` (moe.py:378-482).  With a one-rank
+    group the forward is ``SparseMoeBlock``'s."""
+
+    def __init__(self, hidden_size: int, num_experts: int, num_experts_per_tok: int,
+                 moe_intermediate_size: int, norm_topk_prob: bool = True,
+                 router: nn.Module | None = None, comm_group=None) -> None:
+        SparseMoeBlock.__init__(self, hidden_size, num_experts, num_experts_per_tok,
+                                moe_intermediate_size, norm_topk_prob, router)
+        shard = self._init_tp(comm_group, moe_intermediate_size)
+        self.experts = _Experts(num_experts, hidden_size, shard)
+        self._attach_weight_loaders()
+
+
+class ParallelSparseMoeBlockWithSharedExpert(_TensorParallel, SparseMoeBlockWithSharedExpert):
+    """Tensor-parallel ``SparseMoeBlockWithSharedExpert`` (moe.py:485-591).
+    The shared expert handles its own reduction (a row-parallel MLP built on
+    the same group, as in the reference)."""
+
+    def __init__(self, hidden_size: int, num_experts: int, num_experts_per_tok: int,
+                 moe_intermediate_size: int, shared_expert: nn.Module,
+                 norm_topk_prob: bool = False, router: nn.Module | None = None,
+                 comm_group=None) -> None:
+        SparseMoeBlockWithSharedExpert.__init__(self, hidden_size, num_experts, num_experts_per_tok,
+                                                moe_intermediate_size, shared_expert,
+                                                norm_topk_prob, router)
+        shard = self._init_tp(comm_group, moe_intermediate_size)
+        self.experts = _Experts(num_experts, hidden_size, shard)
+        self._attach_weight_loaders()
