@@ -73,6 +73,9 @@ def parse():
                    help="skip the prefill M=512/2048 and dense N=4096/2048 lines (profiler runs)")
     p.add_argument("--kernel-only", action="store_true",
                    help="launch only the gate_up GEMM in a loop (for profiler runs)")
+    p.add_argument("--profile-prefill", action="store_true",
+                   help="run the config-3 prefill layer eagerly --steps times, no graphs "
+                        "(for rocprofv3 --pmc runs, which count per dispatch)")
     return p.parse_args()
 
 
@@ -290,6 +293,17 @@ def main():
     _lib.load()
 
     base = make_weights(0)
+    if args.profile_prefill:
+        xp, lp = make_inputs(args.prefill_tokens, bias=True, seed=3)
+        layer(xp, lp, base)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            layer(xp, lp, base)
+        torch.cuda.synchronize()
+        print(json.dumps({"prefill_tokens": args.prefill_tokens,
+                          "eager_us": (time.perf_counter() - t0) / args.steps * 1e6}))
+        return
     weights = [base] + [tuple(t.clone() for t in base) for _ in range(W_COPIES - 1)]
     M = args.tokens
     x, logits = make_inputs(M, bias=False)

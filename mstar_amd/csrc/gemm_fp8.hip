@@ -16,8 +16,11 @@
 // step ahead of the math across tile boundaries, so the next tile's first
 // step loads while the current tile's epilogue stores its results; the tile metadata (sorted_ids) arrives
 // the same way, into three rotating LDS buffers.  Rows are 128 bytes with
-// the 16-byte chunks XOR-swizzled by (row & 7), so the lanes of a
-// ds_read_b128 phase hit distinct banks.  One barrier per step.
+// the 16-byte chunks XOR-swizzled by lds_swz(row) = (row & 7) ^ ((row >> 3) & 1):
+// a ds_read_b128 is served 16 lanes (16 consecutive rows) at a time from 64
+// banks, so two rows share a 256-byte bank line and rows r and r + 8 must
+// not use the same chunk -- with (row & 7) alone every fragment read was a
+// two-way conflict (SQ_LDS_BANK_CONFLICT at 48% of SQ_LDS_IDX_ACTIVE).  One barrier per step.
 //
 // Math.  Each wave owns 64 tokens x 128 weight rows as 2 x 4 tiles of
 // 32 x 32, two chained v_mfma_f32_32x32x64_f8f6f4 per tile per step.  The
@@ -59,9 +62,12 @@ constexpr size_t kBigLds = kBigRedOff + (size_t)kBigWN * kBigBM * 4;
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
+// Chunk swizzle of LDS row `row` (see the header comment).
+__device__ __forceinline__ int lds_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
 // 32 bytes: logical 16-byte chunks c and c+1 of swizzled LDS row `row`.
 __device__ __forceinline__ v8i lds_frag_swz(const uint8_t* row_base, int row, int c) {
-  const int sw = row & 7;
+  const int sw = lds_swz(row);
   const v4i lo = *(const v4i*)(row_base + ((c ^ sw) << 4));
   const v4i hi = *(const v4i*)(row_base + (((c + 1) ^ sw) << 4));
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -130,8 +136,11 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   // ---- DMA issue state of the tile the cursor is in.
   // Instruction q of a wave fills tile rows [R, R + 8), R = wave * rows + 8 q:
   // lane l's 16 bytes land at row R + l / 8, physical chunk l % 8, holding
-  // logical chunk (l % 8) ^ (row & 7).  Padding rows read row 0.
+  // logical chunk (l % 8) ^ lds_swz(row); R is a multiple of 8, so that is
+  // (l % 8) ^ (l / 8) ^ ((R / 8) & 1), and R / 8 has the parity of q.
+  // Padding rows read row 0.
   const uint32_t lchunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) * 16);
+  static_assert(BM / 8 % 16 == 0 && BN / 8 % 16 == 0, "a wave's first DMA row is a multiple of 16");
   const uint8_t* a_base = (const uint8_t*)p.A;
   const uint8_t* b_base = (const uint8_t*)p.B;
   uint32_t a_off[AI], b_off[BI];
@@ -163,12 +172,12 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
       const int rr = wave * (BM / 8) + q * 8 + (lane >> 3);
       const int s = slot_of(t, buf, rr);
       const int ar = p.pos_in ? mb * BM + rr : s >= 0 ? s / p.top_k : 0;
-      a_off[q] = (uint32_t)((int64_t)ar * p.lda) + lchunk;
+      a_off[q] = (uint32_t)((int64_t)ar * p.lda) + (lchunk ^ ((q & 1) << 4));
     }
 #pragma unroll
     for (int q = 0; q < BI; ++q) {
       const int br = brow_of(wave * (BN / 8) + q * 8 + (lane >> 3));
-      b_off[q] = (uint32_t)((int64_t)(br >= 0 ? br : 0) * p.ldb) + lchunk;
+      b_off[q] = (uint32_t)((int64_t)(br >= 0 ? br : 0) * p.ldb) + (lchunk ^ ((q & 1) << 4));
     }
     // Scales ride the same DMA stream.  Waves 0-3 move the 256 A-row
     // scales, wave 4 the weight-block scales: lane l the block of (wave
@@ -471,7 +480,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
               const float y0 = x * rc;
               y[e] = clamp_fp8(__builtin_fmaf(__builtin_fmaf(-y0, sc, x), rc, y0));
             }
-            *(int*)(stg + row * 128 + (((cb >> 4) ^ (row & 7)) << 4) + (cb & 15)) =
+            *(int*)(stg + row * 128 + (((cb >> 4) ^ lds_swz(row)) << 4) + (cb & 15)) =
                 cvt_fp8x4(y[0], y[1], y[2], y[3]);
           }
           {  // one lane per token writes the scale; the others' stores fall outside the buffer
@@ -485,7 +494,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
 #pragma unroll
         for (int pass = 0; pass < BM / 8 / 8; ++pass) {  // 8 rows per wave instruction
           const int row = wave * (BM / 8) + pass * 8 + (lane_e >> 3), u = lane_e & 7;
-          const v4i val = *(const v4i*)(stg + row * 128 + ((u ^ (row & 7)) << 4));
+          const v4i val = *(const v4i*)(stg + row * 128 + ((u ^ lds_swz(row)) << 4));
           const int orw = orow(row, slot_of(t, buf, row));
           const uint32_t off = orw >= 0 ? (uint32_t)((int64_t)orw * p.inter + nt * (BN / 2) + u * 16) : kOffNone;
           __builtin_amdgcn_raw_buffer_store_b128(val, rs_cq, off, 0, 0);
