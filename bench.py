@@ -16,8 +16,10 @@ The JSON line also carries:
 * roofline -- the dominant kernel (the gate_up weight-streaming GEMM):
   algorithmic bytes per launch / its mean duration from HIP events on the
   launch stream;
-* prefill -- config 3 at M=8192 (Zipf-biased routing), then M=512 and 2048: us/layer, TFLOP/s and
-  the fraction of dense FP8 peak;
+* prefill -- config 3 at M=8192 (Zipf-biased routing), then M=512 and 2048: us/layer, TFLOP/s,
+  the fraction of dense FP8 peak, and the fraction of HBM peak for the hit experts' weights
+  plus the activations (the Zipf bias concentrates the routing: 28 / 35 / 44 experts are hit
+  at M = 512 / 2048 / 8192, and every token picks expert 0);
 * dense_fp8 -- config 4: the W8A8 dense GEMM (per-token x per-channel
   scales) at M=32 and M=4096 with N=151936 (the LM-head shape);
 * w4a16 -- config 5: the decode layer with int4 group-128 weights at M=32
@@ -137,6 +139,12 @@ def time_graphs(graphs, steps, warmup):
         graphs[i % len(graphs)].replay()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / steps
+
+
+def prefill_bytes(logits, M):
+    """Algorithmic HBM bytes of a prefill layer: every hit expert's FP8 weights and block
+    scales once, the bf16 hidden rows in and the output out, the router logits."""
+    return n_hit(logits) * (EXPERT_FP8_BYTES + EXPERT_SCALE_BYTES) + M * H * 4 + M * E * 4
 
 
 def n_hit(logits):
@@ -367,8 +375,11 @@ def main():
         psec = time_graphs([gp], max(10, args.steps // 10), 3)
         flops = 2.0 * P * K_TOP * EXPERT_FP8_BYTES
         tf = flops / psec / 1e12
+        pbytes = prefill_bytes(lp, P)
         out["prefill"] = {"tokens": P, "us": round(psec * 1e6, 1), "TFLOPs": round(tf, 1),
                           "mfma_fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4),
+                          "algorithmic_bytes": pbytes,
+                          "hbm_frac": round(pbytes / psec / 1e9 / HBM_PEAK_GBS, 4),
                           "workload": "config 3: Zipf-biased routing, same weights"}
         del gp
         # The rest of config 3's shape sweep (M = 512, 2048), same routing bias.
@@ -378,8 +389,11 @@ def main():
             gs, _ = capture(lambda: layer(xs, ls, base))
             ssec = time_graphs([gs], max(20, args.steps // 5), 3)
             tfs = 2.0 * Ms * K_TOP * EXPERT_FP8_BYTES / ssec / 1e12
+            sbytes = prefill_bytes(ls, Ms)
             sweep.append({"tokens": Ms, "us": round(ssec * 1e6, 1), "TFLOPs": round(tfs, 1),
-                          "mfma_fp8_frac": round(tfs / FP8_PEAK_TFLOPS, 4)})
+                          "mfma_fp8_frac": round(tfs / FP8_PEAK_TFLOPS, 4),
+                          "algorithmic_bytes": sbytes,
+                          "hbm_frac": round(sbytes / ssec / 1e9 / HBM_PEAK_GBS, 4)})
             del gs
         if sweep:
             out["prefill_sweep"] = sweep
