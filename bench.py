@@ -215,7 +215,7 @@ def dense_fp8_lines(args, K=2048):
             a = torch.randn(Md, K, generator=g, device="cuda").to(torch.bfloat16)
             aq, sa = ops.quant_fp8_per_token(a)
             gr, _ = capture(lambda: ops.fp8_scaled_mm(aq, sa, wq, ws))
-            sec = time_graphs([gr], 50 if Md == 32 or N < 10000 else 20, 5)
+            sec = time_graphs_median([gr], 50 if Md == 32 or N < 10000 else 20, 10)
             byts = N * K + Md * K + N * 4 + Md * 4 + Md * N * 2
             tf = 2.0 * Md * N * K / sec / 1e12
             res[f"M{Md}"] = {"us": round(sec * 1e6, 1), "GBps": round(byts / sec / 1e9, 1),
@@ -250,7 +250,7 @@ def w4a16_lines(args):
             gr, _ = capture(lambda p1=p1, t1=t1, p2=p2, t2=t2: ops.moe_layer(
                 x, logits, p1, p2, K_TOP, True, 0, _lib.QUANT_W4A16, t1, t2)[0])
             grs.append(gr)
-        sec = time_graphs(grs, 50, 5)
+        sec = time_graphs_median(grs, 50, 10)
         hits = n_hit(logits)
         byts = hits * per_expert + Mw * H * 4 + Mw * E * 4
         tf = 2.0 * Mw * K_TOP * EXPERT_FP8_BYTES / sec / 1e12
