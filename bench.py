@@ -78,6 +78,8 @@ def parse():
     p.add_argument("--profile-prefill", action="store_true",
                    help="run the config-3 prefill layer eagerly --steps times, no graphs "
                         "(for rocprofv3 --pmc runs, which count per dispatch)")
+    p.add_argument("--profile-w4", type=int, default=0, metavar="M",
+                   help="run the config-5 W4A16 layer at M tokens eagerly --steps times (as above)")
     return p.parse_args()
 
 
@@ -306,6 +308,24 @@ def main():
     from mstar_amd import _lib
     _lib.load()
 
+    if args.profile_w4:
+        from mstar_amd import ops, quant
+        g = torch.Generator(device="cuda").manual_seed(9)
+        w1 = torch.randn(E, 2 * INTER, H, generator=g, device="cuda") * 0.02
+        w2 = torch.randn(E, H, INTER, generator=g, device="cuda") * 0.02
+        p1, t1 = quant.quantize_int4_group(w1)
+        p2, t2 = quant.quantize_int4_group(w2)
+        del w1, w2
+        xw, lw = make_inputs(args.profile_w4, bias=False, seed=11)
+        run = lambda: ops.moe_layer(xw, lw, p1, p2, K_TOP, True, 0, _lib.QUANT_W4A16, t1, t2)[0]
+        run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            run()
+        torch.cuda.synchronize()
+        print(json.dumps({"w4_tokens": args.profile_w4, "eager_us": (time.perf_counter() - t0) / args.steps * 1e6}))
+        return
     base = make_weights(0)
     if args.profile_prefill:
         xp, lp = make_inputs(args.prefill_tokens, bias=True, seed=3)
