@@ -41,6 +41,16 @@ constexpr int kW4Lds = 2 * kW4Stage + kW4IdBufs * kW4BM * 4 + 8 * kW4BM * 4;  //
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
+// Token-row chunk swizzle: a row's 16-byte piece l is stored at position
+// l ^ w4_tok_swz(row % 16).  A ds_read_b128 is served in four passes of 16
+// lanes, and the lanes of one pass are a coset of the lane-index subspace
+// spanned by 1, 2, 12 and 24 (measured with SQ_LDS_BANK_CONFLICT on
+// synthetic lane-to-bank maps).  The fragment read of lane (l16, lg) takes
+// piece 4 lg + kc of row 16 i + l16; with this swizzle the 16 lanes of every
+// pass land on 16 different bank quads.  (Plain l ^ row is conflict-free for
+// 16 consecutive lanes but two-way conflicted on these passes.)
+__device__ __forceinline__ int w4_tok_swz(int r) { return r ^ (((r >> 2) & 1) << 3); }
+
 // Logical column (element) at stored position p of a 16-wide segment: each
 // 8-group holds elements 0, 4, 1, 5, 2, 6, 3, 7.
 __device__ __forceinline__ int w4_pair_elem(int p) { return (p & 8) | ((p & 1) << 2) | ((p >> 1) & 3); }
@@ -116,7 +126,7 @@ __global__ __launch_bounds__(kW4Threads) void w4_tile_kernel(GemmArgs p, const f
 
   // ---- DMA of a step into a stage.  Tokens: instruction q of wave w
   // fills rows 8w + 2q + (lane / 32), physical piece lane % 32 holding
-  // logical piece (lane % 32) ^ (row % 16).  Weights: instruction q of wave
+  // logical piece (lane % 32) ^ w4_tok_swz(row % 16).  Weights: instruction q of wave
   // w fills rows 32w + 8q + lane / 8, physical piece lane % 8 holding
   // logical piece (lane % 8) ^ ((row / 2) % 8).  Waves 0-3: the scales of
   // rows 64w + lane; waves 4-5: the token group sums.  setup() points the
@@ -146,7 +156,7 @@ __global__ __launch_bounds__(kW4Threads) void w4_tile_kernel(GemmArgs p, const f
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int tok = 8 * wave + 2 * q + (lane >> 5);
-      const int lp = (lane & 31) ^ (tok & 15);
+      const int lp = (lane & 31) ^ w4_tok_swz(tok & 15);
       a_src[q] = (const uint8_t*)p.A + ((int64_t)arow_of(tok) * p.lda) * 2 + lp * 16;
       const int rho = 32 * wave + 8 * q + (lane >> 3);
       const int wp = (lane & 7) ^ ((rho >> 1) & 7);
@@ -236,7 +246,7 @@ __global__ __launch_bounds__(kW4Threads) void w4_tile_kernel(GemmArgs p, const f
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int tok = 16 * i + l16;
-            const v8s b = *(const v8s*)(sTok + tok * 512 + (((g * 16 + lg * 4 + kc) ^ l16) << 4));
+            const v8s b = *(const v8s*)(sTok + tok * 512 + (((g * 16 + lg * 4 + kc) ^ w4_tok_swz(l16)) << 4));
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) t[i][jj] = mfma_bf16_16x16x32(a[jj], b, t[i][jj]);
           }
