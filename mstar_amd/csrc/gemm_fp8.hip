@@ -16,11 +16,15 @@
 // step ahead of the math across tile boundaries, so the next tile's first
 // step loads while the current tile's epilogue stores its results; the tile metadata (sorted_ids) arrives
 // the same way, into three rotating LDS buffers.  Rows are 128 bytes with
-// the 16-byte chunks XOR-swizzled by lds_swz(row) = (row & 7) ^ ((row >> 3) & 1):
-// a ds_read_b128 is served 16 lanes (16 consecutive rows) at a time from 64
-// banks, so two rows share a 256-byte bank line and rows r and r + 8 must
-// not use the same chunk -- with (row & 7) alone every fragment read was a
-// two-way conflict (SQ_LDS_BANK_CONFLICT at 48% of SQ_LDS_IDX_ACTIVE).  One barrier per step.
+// the 16-byte chunks XOR-swizzled by lds_swz(row) = (row & 7) ^ ((row >> 3) & 1).
+// A ds_read_b128 is served in four passes of 16 lanes, each pass a coset of
+// the lane subspace spanned by 1, 2, 12 and 24 (measured with
+// mstar_amd/microbench/lds_banks.hip).  Two 128-byte rows share a 256-byte
+// bank line, so with (row & 7) alone the bank quad of a fragment read ignored
+// row bits 3-4, and rows r and r ^ 24, which share a pass, collided:
+// every fragment read was a two-way conflict (SQ_LDS_BANK_CONFLICT at 48% of
+// SQ_LDS_IDX_ACTIVE).  The bit-3 term makes the map one-to-one on each pass.
+// One barrier per step.
 //
 // Math.  Each wave owns 64 tokens x 128 weight rows as 2 x 4 tiles of
 // 32 x 32, two chained v_mfma_f32_32x32x64_f8f6f4 per tile per step.  The

@@ -44,10 +44,10 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 // Token-row chunk swizzle: a row's 16-byte piece l is stored at position
 // l ^ w4_tok_swz(row % 16).  A ds_read_b128 is served in four passes of 16
 // lanes, and the lanes of one pass are a coset of the lane-index subspace
-// spanned by 1, 2, 12 and 24 (measured with SQ_LDS_BANK_CONFLICT on
-// synthetic lane-to-bank maps).  The fragment read of lane (l16, lg) takes
-// piece 4 lg + kc of row 16 i + l16; with this swizzle the 16 lanes of every
-// pass land on 16 different bank quads.  (Plain l ^ row is conflict-free for
+// spanned by 1, 2, 12 and 24 (measured with mstar_amd/microbench/lds_banks.hip).
+// The fragment read of lane (l16, lg) takes piece 4 lg + kc of row
+// 16 i + l16; with this swizzle the 16 lanes of every pass land on 16
+// different bank quads.  (Plain l ^ row is conflict-free for
 // 16 consecutive lanes but two-way conflicted on these passes.)
 __device__ __forceinline__ int w4_tok_swz(int r) { return r ^ (((r >> 2) & 1) << 3); }
 

@@ -1,6 +1,9 @@
-"""Build and run the machine-ceiling micro-benchmarks (peak.hip) on the
-current GPU: ``python -m mstar_amd.microbench``.  The binary is written to
-``mstar_amd/_build/peak``."""
+"""Build and run the micro-benchmarks on the current GPU.
+
+``python -m mstar_amd.microbench``      machine ceilings (peak.hip)
+``python -m mstar_amd.microbench lds``  ds_read_b128 lane passes (lds_banks.hip)
+
+Binaries are written to ``mstar_amd/_build/``."""
 from __future__ import annotations
 
 import os
@@ -10,18 +13,23 @@ import sys
 from mstar_amd.build import ARCH, _hipcc
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-OUT = os.path.join(os.path.dirname(HERE), "_build", "peak")
+BUILD = os.path.join(os.path.dirname(HERE), "_build")
+PROGRAMS = {"peak": "peak.hip", "lds": "lds_banks.hip"}
 
 
-def build() -> str:
-    os.makedirs(os.path.dirname(OUT), exist_ok=True)
+def build(name: str = "peak") -> str:
+    out = os.path.join(BUILD, name)
+    os.makedirs(BUILD, exist_ok=True)
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           os.path.join(HERE, "peak.hip"), "-o", OUT]
+           os.path.join(HERE, PROGRAMS[name]), "-o", out]
     subprocess.run(cmd, check=True, capture_output=True)
-    return OUT
+    return out
 
 
 if __name__ == "__main__":
-    exe = OUT if "--no-build" in sys.argv and os.path.exists(OUT) else build()
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    name = args[0] if args else "peak"
+    out = os.path.join(BUILD, name)
+    exe = out if "--no-build" in sys.argv and os.path.exists(out) else build(name)
     sys.exit(subprocess.run([exe]).returncode)
