@@ -49,6 +49,7 @@ namespace mstar {
 
 constexpr int kBigBM = 256, kBigBN = 256;
 constexpr int kBigWM = 4, kBigWN = 2;  // wave grid; wave tile 64 tokens x 128 weight rows
+constexpr int kBigWaves = kBigWM * kBigWN, kBigThreads = 64 * kBigWaves;
 constexpr int kBigStages = 2;
 // Stage: A tile, B tile (128-byte rows), A-row scales [256], weight-block
 // scales [64] (8 used: one per (wave column, 32-row tile)).
@@ -78,10 +79,12 @@ __device__ __forceinline__ v8i lds_frag_swz(const uint8_t* row_base, int row, in
 }
 
 template <int EPI, bool GROUPED, bool BLOCKSCALE>
-__global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
+__global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
   constexpr int BM = kBigBM, BN = kBigBN, WN = kBigWN, WTM = BM / kBigWM, WTN = BN / kBigWN;
   constexpr int MB = WTM / 32, NB = WTN / 32;      // 32x32 MFMA tiles per wave
-  constexpr int AI = BM / 8 / 8, BI = BN / 8 / 8;  // 1 KB DMA instructions per wave per step
+  constexpr int NW = kBigWaves;
+  constexpr int RA = BM / NW, RB = BN / NW;          // A / B tile rows each wave loads
+  constexpr int AI = RA / 8, BI = RB / 8;            // 1 KB DMA instructions per wave per step
   static_assert(EPI != EPI_ACT || NB % 2 == 0, "fused activation pairs gate and up tiles");
   static_assert(WN * NB <= 64, "weight-scale slots");
   extern __shared__ __align__(16) uint8_t smem[];
@@ -119,7 +122,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   // DMA (waves 4-7 move 64 ints each); dense tiles are computed.
   auto issue_ids = [&](int t, int buf) {
     if constexpr (GROUPED) {
-      if (t < total && wave >= 4) {
+      if (t < total && wave >= 4 && wave < 8) {
         const int mb = mb_of(t);
         __builtin_amdgcn_global_load_lds((const void*)(p.sorted_ids + (int64_t)mb * BM + (wave - 4) * 64 + lane),
                                          (lds_void_ptr)(sMeta + buf * kBigMetaInts + (wave - 4) * 64), 4, 0, 0);
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   // (l % 8) ^ (l / 8) ^ ((R / 8) & 1), and R / 8 has the parity of q.
   // Padding rows read row 0.
   const uint32_t lchunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) * 16);
-  static_assert(BM / 8 % 16 == 0 && BN / 8 % 16 == 0, "a wave's first DMA row is a multiple of 16");
+  static_assert(RA % 16 == 0 && RB % 16 == 0, "a wave's first DMA row is a multiple of 16");
   const uint8_t* a_base = (const uint8_t*)p.A;
   const uint8_t* b_base = (const uint8_t*)p.B;
   uint32_t a_off[AI], b_off[BI];
@@ -173,14 +176,14 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     };
 #pragma unroll
     for (int q = 0; q < AI; ++q) {
-      const int rr = wave * (BM / 8) + q * 8 + (lane >> 3);
+      const int rr = wave * RA + q * 8 + (lane >> 3);
       const int s = slot_of(t, buf, rr);
       const int ar = p.pos_in ? mb * BM + rr : s >= 0 ? s / p.top_k : 0;
       a_off[q] = (uint32_t)((int64_t)ar * p.lda) + (lchunk ^ ((q & 1) << 4));
     }
 #pragma unroll
     for (int q = 0; q < BI; ++q) {
-      const int br = brow_of(wave * (BN / 8) + q * 8 + (lane >> 3));
+      const int br = brow_of(wave * RB + q * 8 + (lane >> 3));
       b_off[q] = (uint32_t)((int64_t)(br >= 0 ? br : 0) * p.ldb) + (lchunk ^ ((q & 1) << 4));
     }
     // Scales ride the same DMA stream.  Waves 0-3 move the 256 A-row
@@ -213,7 +216,7 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
         const int s = slot_of(t, buf, wave * 64 + lane);
         __builtin_amdgcn_global_load_lds((const void*)(p.a_scale + (s >= 0 ? s : 0)),
                                          (lds_void_ptr)(meta + BM + wave * 64), 4, 0, 0);
-      } else {
+      } else if (wave < 8) {
         const int c = nt * BN + (wave - 4) * 64 + lane;
         __builtin_amdgcn_global_load_lds((const void*)((const float*)p.b_scale + (c < p.N ? c : 0)),
                                          (lds_void_ptr)(meta + 2 * BM + (wave - 4) * 64), 4, 0, 0);
@@ -226,11 +229,11 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
     uint8_t* st = smem + stage * kBigStageBytes;
     if (n < AI) {
       __builtin_amdgcn_global_load_lds((const void*)(a_base + a_off[n] + kb * 128),
-                                       (lds_void_ptr)(st + (wave * (BM / 8) + n * 8) * 128), 16, 0, 0);
+                                       (lds_void_ptr)(st + (wave * RA + n * 8) * 128), 16, 0, 0);
     } else {
       const int q = n - AI;
       __builtin_amdgcn_global_load_lds((const void*)(b_base + b_off[q] + kb * 128),
-                                       (lds_void_ptr)(st + BM * 128 + (wave * (BN / 8) + q * 8) * 128),
+                                       (lds_void_ptr)(st + BM * 128 + (wave * RB + q * 8) * 128),
                                        16, 0, 0);
     }
     if constexpr (BLOCKSCALE) {
@@ -299,9 +302,9 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
   // count, waited for in full).
   int epi_stores;
   if constexpr (EPI == EPI_ACT)
-    epi_stores = p.cq ? BM / 8 / 8 + MB : ((p.ldc & 7) == 0 && (p.inter & 7) == 0) ? BM / 8 / 4 : 0;
+    epi_stores = p.cq ? RA / 8 + MB : ((p.ldc & 7) == 0 && (p.inter & 7) == 0) ? RA / 4 : 0;
   else
-    epi_stores = ((p.ldc & 7) == 0 && (p.N & 7) == 0) ? MB * 8 : 0;
+    epi_stores = ((p.ldc & 7) == 0 && (p.N & 7) == 0) ? MB * (BM / 2 / NW / 2) : 0;
 
   for (int j = 0; tile_of(j) < total; ++j) {
     const int t = tile_of(j);
@@ -324,9 +327,10 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
       // Step q is the only DMA in flight: wait for it.  At a tile's first
       // step the previous epilogue's stores, issued after it, may still be
       // draining: they are left in flight.
-      if (kb == 0 && j > 0 && epi_stores == MB * 8) wait_vmcnt<MB * 8>();
-      else if (kb == 0 && j > 0 && epi_stores == BM / 8 / 4) wait_vmcnt<BM / 8 / 4>();
-      else if (kb == 0 && j > 0 && epi_stores == BM / 8 / 8 + MB) wait_vmcnt<BM / 8 / 8 + MB>();
+      constexpr int kStStore = MB * (BM / 2 / NW / 2), kStAct = RA / 4, kStQuant = RA / 8 + MB;
+      if (kb == 0 && j > 0 && EPI != EPI_ACT && epi_stores == kStStore) wait_vmcnt<kStStore>();
+      else if (kb == 0 && j > 0 && EPI == EPI_ACT && epi_stores == kStAct) wait_vmcnt<kStAct>();
+      else if (kb == 0 && j > 0 && EPI == EPI_ACT && epi_stores == kStQuant) wait_vmcnt<kStQuant>();
       else wait_vmcnt<0>();
       // Step q has landed for every wave, and every wave is past step q-1,
       // whose stage the next issue overwrites.
@@ -496,8 +500,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
         }
         lds_sync();
 #pragma unroll
-        for (int pass = 0; pass < BM / 8 / 8; ++pass) {  // 8 rows per wave instruction
-          const int row = wave * (BM / 8) + pass * 8 + (lane_e >> 3), u = lane_e & 7;
+        for (int pass = 0; pass < RA / 8; ++pass) {  // 8 rows per wave instruction
+          const int row = wave * RA + pass * 8 + (lane_e >> 3), u = lane_e & 7;
           const v4i val = *(const v4i*)(stg + row * 128 + ((u ^ lds_swz(row)) << 4));
           const int orw = orow(row, slot_of(t, buf, row));
           const uint32_t off = orw >= 0 ? (uint32_t)((int64_t)orw * p.inter + nt * (BN / 2) + u * 16) : kOffNone;
@@ -522,8 +526,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
         }
         lds_sync();
 #pragma unroll
-        for (int pass = 0; pass < BM / 8 / 4; ++pass) {  // 4 rows per wave instruction
-          const int row = wave * (BM / 8) + pass * 4 + (lane_e >> 4), u = lane_e & 15;
+        for (int pass = 0; pass < RA / 4; ++pass) {  // 4 rows per wave instruction
+          const int row = wave * RA + pass * 4 + (lane_e >> 4), u = lane_e & 15;
           const v4i val = *(const v4i*)(stg + row * 256 + ((u ^ (row & 15)) << 4));
           const int orw = orow(row, slot_of(t, buf, row));
           const int gcol = nt * (BN / 2) + u * 8;
@@ -581,8 +585,8 @@ __global__ __launch_bounds__(512) void gemm_fp8_big_kernel(GemmArgs p) {
           }
           lds_sync();
 #pragma unroll
-          for (int pass = 0; pass < 8; ++pass) {  // 2 rows per wave instruction
-            const int lr2 = wave * 16 + pass * 2 + (lane_e >> 5), u = lane_e & 31;
+          for (int pass = 0; pass < BM / 2 / NW / 2; ++pass) {  // 2 rows per wave instruction
+            const int lr2 = wave * (BM / 2 / NW) + pass * 2 + (lane_e >> 5), u = lane_e & 31;
             const v4i val = *(const v4i*)(stg + lr2 * 512 + ((u ^ (lr2 & 31)) << 4));
             const int orw = orow((lr2 >> 5) * WTM + i * 32 + (lr2 & 31), slot_of(t, buf, (lr2 >> 5) * WTM + i * 32 + (lr2 & 31)));
             const int col = nt * BN + u * 8;
@@ -626,7 +630,7 @@ static int run_big(const GemmArgs& a, hipStream_t stream) {
   if (st != kOk) return st;
   // Persistent: one workgroup per CU (the LDS ring allows no more).
   const int64_t grid = device_cu_count();
-  kern<<<dim3((unsigned)grid), dim3(512), kBigLds, stream>>>(a);
+  kern<<<dim3((unsigned)grid), dim3(kBigThreads), kBigLds, stream>>>(a);
   return launch_status("gemm_fp8_big");
 }
 
