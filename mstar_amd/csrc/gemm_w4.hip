@@ -238,17 +238,32 @@ __global__ __launch_bounds__(kW4Threads) void w4_tile_kernel(GemmArgs p, const f
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) t[i][jj] = v4f{0.f, 0.f, 0.f, 0.f};
+        // Token fragments one K-chunk ahead: the reads of chunk kc + 1 are
+        // in flight while chunk kc's MFMAs run.
+        auto tok_frag = [&](int i, int kc) -> v8s {
+          return *(const v8s*)(sTok + (16 * i + l16) * 512 + (((g * 16 + lg * 4 + kc) ^ w4_tok_swz(l16)) << 4));
+        };
+        v8s bcur[4], bnxt[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bcur[i] = tok_frag(i, 0);
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
+          if (kc + 1 < 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bnxt[i] = tok_frag(i, kc + 1);
+          }
+          __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this chunk's MFMAs
           v8s a[2];
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) a[jj] = int4x8_bias128((uint32_t)wq[jj][kc], k4);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int tok = 16 * i + l16;
-            const v8s b = *(const v8s*)(sTok + tok * 512 + (((g * 16 + lg * 4 + kc) ^ w4_tok_swz(l16)) << 4));
+          for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) t[i][jj] = mfma_bf16_16x16x32(a[jj], b, t[i][jj]);
+            for (int jj = 0; jj < 2; ++jj) t[i][jj] = mfma_bf16_16x16x32(a[jj], bcur[i], t[i][jj]);
+          __builtin_amdgcn_sched_barrier(0);
+          if (kc + 1 < 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bcur[i] = bnxt[i];
           }
         }
         // s (t - 136 sum x) per (row, token): rows 4 lg + r, token 16 i + l16.
