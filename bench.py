@@ -217,13 +217,26 @@ def dense_fp8_lines(args, K=2048):
             a = torch.randn(Md, K, generator=g, device="cuda").to(torch.bfloat16)
             aq, sa = ops.quant_fp8_per_token(a)
             gr, _ = capture(lambda: ops.fp8_scaled_mm(aq, sa, wq, ws))
-            sec = time_graphs_median([gr], 50 if Md == 32 or N < 10000 else 20, 10)
+            steps = 50 if Md == 32 or N < 10000 else 20
+            sec = time_graphs_median([gr], steps, 10)
             byts = N * K + Md * K + N * 4 + Md * 4 + Md * N * 2
             tf = 2.0 * Md * N * K / sec / 1e12
             res[f"M{Md}"] = {"us": round(sec * 1e6, 1), "GBps": round(byts / sec / 1e9, 1),
                              "hbm_frac": round(byts / sec / 1e9 / HBM_PEAK_GBS, 4), "TFLOPs": round(tf, 1),
                              "mfma_fp8_frac": round(tf / FP8_PEAK_TFLOPS, 4)}
             del gr
+            # The vendor library on the same operands (hipBLASLt through
+            # torch._scaled_mm, row-wise scales): a reference point, not a
+            # path of this library.
+            try:
+                sa2, ws2 = sa.reshape(Md, 1).contiguous(), ws.reshape(1, N).contiguous()
+                grl, _ = capture(lambda: torch._scaled_mm(aq, wq.t(), scale_a=sa2, scale_b=ws2,
+                                                          out_dtype=torch.bfloat16))
+                res[f"M{Md}"]["hipblaslt_us"] = round(time_graphs_median([grl], steps, 10) * 1e6, 1)
+                del grl
+            except Exception as ex:  # library without row-wise FP8 scaling
+                res[f"M{Md}"]["hipblaslt_us"] = None
+                res[f"M{Md}"]["hipblaslt_error"] = f"{type(ex).__name__}: {str(ex)[:120]}"
         return res
 
     res = one_n(151936)
