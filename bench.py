@@ -20,8 +20,11 @@ The JSON line also carries:
   the fraction of dense FP8 peak, and the fraction of HBM peak for the hit experts' weights
   plus the activations (the Zipf bias concentrates the routing: 28 / 35 / 44 experts are hit
   at M = 512 / 2048 / 8192, and every token picks expert 0);
+  prefill.library_reference times hipBLASLt on plain GEMMs with the same
+  FLOPs as the layer's two GEMMs (a reference point for the MFMA roofline);
 * dense_fp8 -- config 4: the W8A8 dense GEMM (per-token x per-channel
-  scales) at M=32 and M=4096 with N=151936 (the LM-head shape);
+  scales) at M=32 and M=4096 with N=151936 (the LM-head shape), each line
+  with hipBLASLt's time on the same operands;
 * w4a16 -- config 5: the decode layer with int4 group-128 weights at M=32
   and M=1024;
 * cpu_baseline -- the reference's CPU MoE path (TopKRouter + the per-expert
@@ -246,6 +249,40 @@ def dense_fp8_lines(args, K=2048):
     return res
 
 
+def prefill_library_reference(P):
+    """Reference point for config 3's MFMA roofline: hipBLASLt (torch._scaled_mm,
+    row-wise scales) on plain, ungrouped GEMMs with the prefill layer's FLOPs --
+    [P*k, H] x [2I, H]^T (gate_up) and [P*k, I] x [H, I]^T (down) -- beside
+    this library's dense kernel on the same operands.  No gather, padding,
+    block scales or fused epilogue: an easier problem than the grouped layer."""
+    from mstar_amd import ops, quant
+    g = torch.Generator(device="cuda").manual_seed(3)
+    res = {}
+    for name, (Mr, N, Kr) in (("gate_up_equivalent", (P * K_TOP, 2 * INTER, H)),
+                              ("down_equivalent", (P * K_TOP, H, INTER))):
+        wq, ws = quant.quantize_fp8_per_channel(torch.randn(N, Kr, generator=g, device="cuda") * 0.02)
+        aq, sa = ops.quant_fp8_per_token(torch.randn(Mr, Kr, generator=g, device="cuda").to(torch.bfloat16))
+        fl = 2.0 * Mr * N * Kr
+        gr, _ = capture(lambda: ops.fp8_scaled_mm(aq, sa, wq, ws))
+        ours = time_graphs_median([gr], 20, 10)
+        del gr
+        entry = {"shape": [Mr, N, Kr], "this_library_dense_us": round(ours * 1e6, 1),
+                 "this_library_mfma_fp8_frac": round(fl / ours / 1e12 / FP8_PEAK_TFLOPS, 4)}
+        try:
+            sa2, ws2 = sa.reshape(Mr, 1).contiguous(), ws.reshape(1, N).contiguous()
+            grl, _ = capture(lambda: torch._scaled_mm(aq, wq.t(), scale_a=sa2, scale_b=ws2,
+                                                      out_dtype=torch.bfloat16))
+            lib = time_graphs_median([grl], 20, 10)
+            del grl
+            entry.update({"hipblaslt_us": round(lib * 1e6, 1),
+                          "hipblaslt_mfma_fp8_frac": round(fl / lib / 1e12 / FP8_PEAK_TFLOPS, 4)})
+        except Exception as ex:  # library without row-wise FP8 scaling
+            entry.update({"hipblaslt_us": None, "hipblaslt_error": f"{type(ex).__name__}: {str(ex)[:120]}"})
+        res[name] = entry
+        del wq, ws, aq, sa
+    return res
+
+
 def w4a16_lines(args):
     """Config 5: the decode layer with int4 group-128 weights (bf16 scales),
     routing from logits, two rotated weight copies."""
@@ -436,6 +473,8 @@ def main():
             del gs
         if sweep:
             out["prefill_sweep"] = sweep
+        if not args.no_sweep and not args.no_extra:
+            out["prefill"]["library_reference"] = prefill_library_reference(P)
 
     if not args.no_extra:
         del weights, graphs
