@@ -15,8 +15,10 @@ is checked, bit for bit, with no tolerance:
   output: the expert order changes every block offset and position, not the
   arithmetic of any slot.
 
-The oracle comparisons of these paths are in test_gpu_moe.py; these checks
-cover the rows and orderings that those score only on a subset."""
+The dense W8A8 GEMM gets the matching checks over its whole output at the
+LM-head shape.  The oracle comparisons of these paths are in test_gpu_moe.py
+and test_gpu_dense_quant.py; these checks cover the rows and orderings that
+those score only on a subset."""
 from __future__ import annotations
 
 import functools
@@ -115,3 +117,24 @@ def test_expert_relabelling_is_exact(M, quant):
     base = _run(quant, x, tw, ti)
     moved = _run(quant, x, tw, sigma[ti].contiguous(), weights=relabelled)
     assert torch.equal(_bits(moved), _bits(base))
+
+
+@pytest.mark.parametrize("M,N", [(4096, 151936), (32, 151936), (4096, 2048)])
+def test_dense_fp8_properties_are_exact(M, N):
+    """The dense W8A8 GEMM (y = bf16((A_q . W_q^T) s_a s_w)) over its whole
+    output: permuting tokens and weight rows permutes the output's rows and
+    columns, and doubling the per-channel scales doubles it."""
+    from mstar_amd import ops, quant
+    K = 2048
+    g = torch.Generator(device=DEV).manual_seed(N + M)
+    wq, ws = quant.quantize_fp8_per_channel(torch.randn(N, K, generator=g, device=DEV) * 0.02)
+    aq, sa = ops.quant_fp8_per_token(torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16))
+    print(f"properties: dense M={M} N={N}", flush=True)
+    base = ops.fp8_scaled_mm(aq, sa, wq, ws)
+    pm = torch.randperm(M, generator=torch.Generator().manual_seed(1)).to(DEV)
+    pn = torch.randperm(N, generator=torch.Generator().manual_seed(2)).to(DEV)
+    moved = ops.fp8_scaled_mm(aq[pm].contiguous(), sa[pm].contiguous(), wq[pn].contiguous(), ws[pn].contiguous())
+    assert torch.equal(_bits(moved), _bits(base[pm][:, pn]))
+    doubled = ops.fp8_scaled_mm(aq, sa, wq, ws * 2)
+    assert torch.isfinite(base.float()).all()
+    assert torch.equal(_bits(doubled), _bits((base.float() * 2).to(torch.bfloat16)))
