@@ -220,6 +220,30 @@ def test_moe_layer_prefill_8192_zipf_rows():
     assert_moe_close(out.cpu()[rows], ref, what="moe_layer fp8 M=8192 zipf rows")
 
 
+@pytest.mark.parametrize("M", [16384, 65536])
+def test_moe_layer_large_batches(M):
+    """Batches past the bench's prefill point (131072 and 524288 slots): the
+    grid-wide routing over 512 / 2048 workgroups, 32-bit position offsets
+    and the 256-row GEMMs at eight times the M=8192 tile count.  Routing is
+    checked whole; the oracle scores the first and last 64 rows and 128 in
+    between."""
+    from mstar_amd import _lib, ops
+    H, E, I, k = 2048, 128, 768, 8
+    q1, s1, q2, s2 = _fp8_weights(H, E, I)
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    logits = torch.randn(M, E, generator=g) + O.zipf_bias(E)
+    rw, rids = O.router_topk_softmax(logits, k, True)
+    print(f"moe_layer large batch M={M}", flush=True)
+    out, tw, ti = ops.moe_layer(x.to(DEV), logits.to(DEV), q1, q2, k, True, 0, _lib.QUANT_FP8_W8A8,
+                                s1, s2)
+    assert torch.equal(ti.cpu(), rids)
+    rows = torch.cat([torch.arange(64), torch.randint(0, M, (128,), generator=g),
+                      torch.arange(M - 64, M)]).unique()
+    ref = _fp8_ref(x[rows], q1, s1, q2, s2, rw[rows], rids[rows])
+    assert_moe_close(out.cpu()[rows], ref, what=f"moe_layer fp8 M={M} zipf rows")
+
+
 @pytest.mark.parametrize("reduce", [True, False])
 def test_fused_experts_fp8_position_rows(reduce):
     """4096 tokens x top-8 over 128 experts: the 256-row FP8 kernel stores the
