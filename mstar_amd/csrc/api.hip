@@ -51,6 +51,13 @@ static int choose_bm(int64_t slots, int E, bool fp8) {
   return 128;
 }
 
+// 128-row FP8 tiles below this many slots per expert on average (set from
+// the prefill layer's times at E=128, top-8, M = 512 .. 8192).
+#ifndef MSTAR_BIG_HALF_MAX_AVG
+#define MSTAR_BIG_HALF_MAX_AVG 128
+#endif
+constexpr int kBigHalfMaxAvg = MSTAR_BIG_HALF_MAX_AVG;
+
 // Largest token count served by the weight-streaming kernels.
 constexpr int64_t kStreamMaxTokens = 64;
 
@@ -68,6 +75,8 @@ struct Plan {
   bool by_pos = false;
   // W4A16 above decode size: the 64-token int4 tile GEMM (gemm_w4.hip).
   bool w4_tile = false;
+  // FP8 on the persistent tile GEMM (gemm_fp8.hip), bm = 256 or 128 rows.
+  bool big = false;
   int bm = 16;
   int64_t slots = 0, max_padded = 0, max_blocks = 0;
   size_t off_sorted, off_eids, off_ntpp, off_eoff, off_ecnt, off_c2, off_c3, off_hq, off_hs,
@@ -106,6 +115,11 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
                   (quant == MSTAR_QUANT_W4A16 && H % 256 == 0 && I % 256 == 0));
   pl->w4_tile = quant == MSTAR_QUANT_W4A16 && !pl->stream && w4_tile_supported(H, I);
   pl->bm = pl->stream ? 16 : pl->w4_tile ? 64 : choose_bm(pl->slots, E, quant == MSTAR_QUANT_FP8_W8A8);
+  pl->big = quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream && pl->bm == kBigBlockM;
+  // Up to kBigHalfMaxAvg slots per expert on average, 128-row tiles: half the
+  // padding per expert and twice the tiles, so the last round of tiles over
+  // the CUs wastes less.
+  if (pl->big && pl->slots < (int64_t)kBigHalfMaxAvg * E) pl->bm = kBigBlockM / 2;
   pl->max_padded = pl->slots + (int64_t)E * (pl->bm - 1);
   pl->max_blocks = (pl->max_padded + pl->bm - 1) / pl->bm;
   size_t o = 0;
@@ -116,7 +130,7 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->off_eoff = take((size_t)(E + 1) * 4);
   pl->off_ecnt = take((size_t)E * 4);
   const bool fp8_tiled = quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream;
-  pl->by_pos = fp8_tiled && pl->bm == kBigBlockM;
+  pl->by_pos = fp8_tiled && pl->big;
   // Rows of the position-indexed buffers: every position of every block.
   const size_t pos_rows = (size_t)pl->max_blocks * pl->bm;
   pl->off_c2 = pl->by_pos ? 0 : take((size_t)pl->slots * I * 2);
@@ -233,7 +247,7 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
     g1.A = hq; g1.lda = H; g1.a_scale = hs; g1.ld_as = H / 128;
     // The 256-row kernel quantises the activation output in its epilogue;
     // the smaller tiles store bf16 and a quantisation launch follows.
-    const bool fused_q = pl.bm == kBigBlockM;
+    const bool fused_q = pl.big;
     if (fused_q) { g1.cq = cq; g1.cs = cs; }
     if (pl.by_pos) {
       g1.pos_out = 1;
@@ -241,14 +255,16 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
       g2.pos_in = 1;
       g2.pos_out = reduce_results;
     }
-    st = launch_tile_gemm(g1, A_FP8G, B_FP8BLK, EPI_ACT, act_dtype, true, pl.bm, stream);
+    st = pl.big ? launch_gemm_fp8_big(g1, EPI_ACT, true, pl.bm, stream)
+                : launch_tile_gemm(g1, A_FP8G, B_FP8BLK, EPI_ACT, act_dtype, true, pl.bm, stream);
     if (st != kOk) return st;
     if (!fused_q) {
       st = launch_quant_fp8_group(cache2, act_dtype, pl.slots, I, I, cq, cs, stream);
       if (st != kOk) return st;
     }
     g2.A = cq; g2.lda = I; g2.a_scale = cs; g2.ld_as = I / 128;
-    st = launch_tile_gemm(g2, A_FP8G, B_FP8BLK, EPI_STORE, act_dtype, true, pl.bm, stream);
+    st = pl.big ? launch_gemm_fp8_big(g2, EPI_STORE, true, pl.bm, stream)
+                : launch_tile_gemm(g2, A_FP8G, B_FP8BLK, EPI_STORE, act_dtype, true, pl.bm, stream);
     if (st != kOk) return st;
   } else if (pl.w4_tile) {
     uint16_t* hp = (uint16_t*)(ws + pl.off_w4h);
@@ -420,8 +436,15 @@ int mstar_fp8_scaled_mm(const uint8_t* a, const float* a_scale, const uint8_t* w
     const int st = launch_dense_stream(g, (hipStream_t)stream);
     if (st != kUnsupported) return st;  // else the tile kernel below
   }
-  const int bm = M <= 32 ? 32 : M <= 64 ? 64 : kBigBlockM;
-  return launch_tile_gemm(g, A_FP8R, B_FP8R, EPI_DENSE, kBF16, false, bm, (hipStream_t)stream);
+  if (M > 64) {
+    // 256-row tiles, or 128-row tiles when the 256-row ones would not give
+    // every CU a tile (N=2048 at M=4096: 128 tiles of 256 rows for 256 CUs).
+    const int64_t tiles256 = ((M + kBigBlockM - 1) / kBigBlockM) * ((N + 255) / 256);
+    const int bm = tiles256 < device_cu_count() ? kBigBlockM / 2 : kBigBlockM;
+    return launch_gemm_fp8_big(g, EPI_DENSE, false, bm, (hipStream_t)stream);
+  }
+  return launch_tile_gemm(g, A_FP8R, B_FP8R, EPI_DENSE, kBF16, false, M <= 32 ? 32 : 64,
+                          (hipStream_t)stream);
 }
 
 int mstar_moe_grouped_gemm(const void* A, const void* B, void* C, const void* topk_weights,

@@ -47,23 +47,29 @@
 
 namespace mstar {
 
-constexpr int kBigBM = 256, kBigBN = 256;
-constexpr int kBigWM = 4, kBigWN = 2;  // wave grid; wave tile 64 tokens x 128 weight rows
-constexpr int kBigWaves = kBigWM * kBigWN, kBigThreads = 64 * kBigWaves;
+constexpr int kBigBN = 256, kBigWaves = 8, kBigThreads = 64 * kBigWaves;
 constexpr int kBigStages = 2;
-// Stage: A tile, B tile (128-byte rows), A-row scales [256], weight-block
-// scales [64] (8 used: one per (wave column, 32-row tile)).
-constexpr int kBigAsOff = (kBigBM + kBigBN) * 128;
-constexpr int kBigBsOff = kBigAsOff + kBigBM * 4;
-constexpr int kBigStageBytes = kBigBsOff + 64 * 4;
-// Tile metadata buffer: slot of each row [BM] (grouped), the epilogue's row
-// factors [BM] (routed weight or dense A-row scale) and column factors [BN]
-// (dense weight scales).
-constexpr int kBigMetaInts = 2 * kBigBM + kBigBN;
 constexpr int kBigIdBufs = 3;
-// Per-token amax exchange between the two wave columns (fused quantisation).
-constexpr size_t kBigRedOff = (size_t)kBigStages * kBigStageBytes + (size_t)kBigIdBufs * kBigMetaInts * 4;
-constexpr size_t kBigLds = kBigRedOff + (size_t)kBigWN * kBigBM * 4;
+// Tile geometry for BM = 256 or 128 token rows (one alignment block) x 256
+// weight rows, 8 waves of 64 tokens: a 4 x 2 wave grid of 64 x 128 wave
+// tiles (BM = 256) or 2 x 4 of 64 x 64 (BM = 128).
+template <int BM>
+struct BigCfg {
+  static_assert(BM == 256 || BM == 128, "tile rows");
+  static constexpr int WM = BM / 64, WN = kBigWaves / WM;  // wave grid
+  // Stage: A tile, B tile (128-byte rows), A-row scales [BM], weight-block
+  // scales [64] (WN * NB used: one per (wave column, 32-row tile)).
+  static constexpr int AsOff = (BM + kBigBN) * 128;
+  static constexpr int BsOff = AsOff + BM * 4;
+  static constexpr int StageBytes = BsOff + 64 * 4;
+  // Tile metadata buffer: slot of each row [BM] (grouped), the epilogue's
+  // row factors [BM] (routed weight or dense A-row scale) and column factors
+  // [BN] (dense weight scales).
+  static constexpr int MetaInts = 2 * BM + kBigBN;
+  // Per-token amax exchange between the wave columns (fused quantisation).
+  static constexpr size_t RedOff = (size_t)kBigStages * StageBytes + (size_t)kBigIdBufs * MetaInts * 4;
+  static constexpr size_t Lds = RedOff + (size_t)WN * BM * 4;
+};
 
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
@@ -78,9 +84,14 @@ __device__ __forceinline__ v8i lds_frag_swz(const uint8_t* row_base, int row, in
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-template <int EPI, bool GROUPED, bool BLOCKSCALE>
+template <int EPI, bool GROUPED, bool BLOCKSCALE, int BM>
 __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
-  constexpr int BM = kBigBM, BN = kBigBN, WN = kBigWN, WTM = BM / kBigWM, WTN = BN / kBigWN;
+  using Cfg = BigCfg<BM>;
+  constexpr int BN = kBigBN, WN = Cfg::WN, WTM = BM / Cfg::WM, WTN = BN / WN;
+  constexpr int kBigAsOff = Cfg::AsOff, kBigBsOff = Cfg::BsOff, kBigStageBytes = Cfg::StageBytes;
+  constexpr int kBigMetaInts = Cfg::MetaInts;
+  constexpr size_t kBigRedOff = Cfg::RedOff;
+  constexpr int RW = BM / 64;  // waves that move one int per tile row (64 rows each)
   constexpr int MB = WTM / 32, NB = WTN / 32;      // 32x32 MFMA tiles per wave
   constexpr int NW = kBigWaves;
   constexpr int RA = BM / NW, RB = BN / NW;          // A / B tile rows each wave loads
@@ -122,7 +133,7 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
   // DMA (waves 4-7 move 64 ints each); dense tiles are computed.
   auto issue_ids = [&](int t, int buf) {
     if constexpr (GROUPED) {
-      if (t < total && wave >= 4 && wave < 8) {
+      if (t < total && wave >= 4 && wave < 4 + RW) {
         const int mb = mb_of(t);
         __builtin_amdgcn_global_load_lds((const void*)(p.sorted_ids + (int64_t)mb * BM + (wave - 4) * 64 + lane),
                                          (lds_void_ptr)(sMeta + buf * kBigMetaInts + (wave - 4) * 64), 4, 0, 0);
@@ -186,11 +197,11 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
       const int br = brow_of(wave * RB + q * 8 + (lane >> 3));
       b_off[q] = (uint32_t)((int64_t)(br >= 0 ? br : 0) * p.ldb) + (lchunk ^ ((q & 1) << 4));
     }
-    // Scales ride the same DMA stream.  Waves 0-3 move the 256 A-row
+    // Scales ride the same DMA stream.  Waves 0 .. RW-1 move the BM A-row
     // scales, wave 4 the weight-block scales: lane l the block of (wave
     // column (l / NB) % WN, 32-row tile l % NB).
     if constexpr (BLOCKSCALE) {
-      if (wave < 4) {
+      if (wave < RW) {
         const int s = slot_of(t, buf, wave * 64 + lane);
         sc_src = p.a_scale + (int64_t)(p.pos_in ? mb * BM + wave * 64 + lane : s >= 0 ? s / p.top_k : 0) * p.ld_as;
       } else if (wave == 4) {
@@ -206,17 +217,17 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
     // and column scales.
     int* meta = sMeta + buf * kBigMetaInts;
     if constexpr (EPI == EPI_STORE) {
-      if (p.mul_routed && p.topk_w_dtype == kF32 && wave < 4) {
+      if (p.mul_routed && p.topk_w_dtype == kF32 && wave < RW) {
         const int s = slot_of(t, buf, wave * 64 + lane);
         __builtin_amdgcn_global_load_lds((const void*)((const float*)p.topk_w + (s >= 0 ? s : 0)),
                                          (lds_void_ptr)(meta + BM + wave * 64), 4, 0, 0);
       }
     } else if constexpr (EPI == EPI_DENSE) {
-      if (wave < 4) {
+      if (wave < RW) {
         const int s = slot_of(t, buf, wave * 64 + lane);
         __builtin_amdgcn_global_load_lds((const void*)(p.a_scale + (s >= 0 ? s : 0)),
                                          (lds_void_ptr)(meta + BM + wave * 64), 4, 0, 0);
-      } else if (wave < 8) {
+      } else if (wave >= 4 && wave < 8) {
         const int c = nt * BN + (wave - 4) * 64 + lane;
         __builtin_amdgcn_global_load_lds((const void*)((const float*)p.b_scale + (c < p.N ? c : 0)),
                                          (lds_void_ptr)(meta + 2 * BM + (wave - 4) * 64), 4, 0, 0);
@@ -238,7 +249,7 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
     }
     if constexpr (BLOCKSCALE) {
       if (n == 0) {
-        if (wave < 4)
+        if (wave < RW)
           __builtin_amdgcn_global_load_lds((const void*)(sc_src + kb),
                                            (lds_void_ptr)(st + kBigAsOff + wave * 256), 4, 0, 0);
         else if (wave == 4)
@@ -248,7 +259,18 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
     }
   };
   constexpr int kParts = AI + BI;
-  static_assert(kParts == MB * NB, "one DMA instruction per 32x32 tile of the step");
+  constexpr int kTiles = MB * NB;  // 32x32 tiles a wave computes per step
+  static_assert(kParts >= kTiles, "at least one DMA instruction per 32x32 tile of the step");
+  // DMA instructions issued after 32x32 tile ti of a step: parts
+  // [ti * kParts / kTiles, (ti + 1) * kParts / kTiles).
+  auto issue_after = [&](int ti, int kb, int stage) {
+    if constexpr (kParts == kTiles) {
+      issue_part(ti, kb, stage);
+    } else {
+#pragma unroll
+      for (int n = ti * kParts / kTiles; n < (ti + 1) * kParts / kTiles; ++n) issue_part(n, kb, stage);
+    }
+  };
 
   // ---- cursor: tile round ji, step ki, global step qi (ring stage qi % 2).
   // advance() moves it to the next step (set-up of a new tile included) and
@@ -379,7 +401,7 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
             v16f tt = mfma_fp8_32x32x64(w[0], x[i][0], v16f{});
             tt = mfma_fp8_32x32x64(w[1], x[i][1], tt);
             if (i == MB - 1 && jj + 1 < NB) load_w(jj + 1, wf[0]);
-            issue_part(jj * MB + i, ik, ist);
+            issue_after(jj * MB + i, ik, ist);
             const float f = sa[i] * sw[jj];
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][jj][e] = __builtin_fmaf(tt[e], f, acc[i][jj][e]);
@@ -394,7 +416,7 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
 #pragma unroll
           for (int i = 0; i < MB; ++i) {
             acc[i][jj] = mfma_fp8_32x32x64(w[1], x[i][1], acc[i][jj]);
-            issue_part(jj * MB + i, ik, ist);
+            issue_after(jj * MB + i, ik, ist);
           }
           if (jj + 1 < NB) load_w(jj + 1, wf[0]);
         }
@@ -421,7 +443,7 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
     auto orow = [&](int row, int slot) -> int {
       return slot < 0 ? -1 : p.pos_out ? mb * BM + row : slot;
     };
-    if (GROUPED && p.pos_of && nt == 0 && wave < 4) {
+    if (GROUPED && p.pos_of && nt == 0 && wave < RW) {
       // Position of each slot of the m-block (one buffer store per wave:
       // extra stores only make the next tile's first wait stricter).
       const int row = wave * 64 + lane_e, slot = slot_of(t, buf, row);
@@ -623,23 +645,40 @@ __global__ __launch_bounds__(kBigThreads) void gemm_fp8_big_kernel(GemmArgs p) {
   wait_vmcnt<0>();  // no DMA outlives the kernel
 }
 
-template <int EPI, bool GROUPED, bool BLOCKSCALE>
+template <int EPI, bool GROUPED, bool BLOCKSCALE, int BM>
 static int run_big(const GemmArgs& a, hipStream_t stream) {
-  auto kern = gemm_fp8_big_kernel<EPI, GROUPED, BLOCKSCALE>;
-  const int st = ensure_dynamic_lds((const void*)kern, kBigLds, "gemm_fp8_big");
+  auto kern = gemm_fp8_big_kernel<EPI, GROUPED, BLOCKSCALE, BM>;
+  constexpr size_t lds = BigCfg<BM>::Lds;
+  const int st = ensure_dynamic_lds((const void*)kern, lds, "gemm_fp8_big");
   if (st != kOk) return st;
   // Persistent: one workgroup per CU (the LDS ring allows no more).
   const int64_t grid = device_cu_count();
-  kern<<<dim3((unsigned)grid), dim3(kBigThreads), kBigLds, stream>>>(a);
+  kern<<<dim3((unsigned)grid), dim3(kBigThreads), lds, stream>>>(a);
   return launch_status("gemm_fp8_big");
 }
 
-int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t stream) {
+template <int BM>
+static int run_big_bm(const GemmArgs& a, int epi, bool grouped, hipStream_t stream) {
+  if (grouped) {
+    if (epi == EPI_ACT) return run_big<EPI_ACT, true, true, BM>(a, stream);
+    if (epi == EPI_STORE) return run_big<EPI_STORE, true, true, BM>(a, stream);
+  } else if (epi == EPI_DENSE) {
+    return run_big<EPI_DENSE, false, false, BM>(a, stream);
+  }
+  set_last_error("gemm_fp8_big: unsupported epilogue %d (grouped=%d)", epi, (int)grouped);
+  return kUnsupported;
+}
+
+int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, int bm, hipStream_t stream) {
+  if (bm != 256 && bm != 128) {
+    set_last_error("gemm_fp8_big: tile rows must be 256 or 128 (got %d)", bm);
+    return kInvalidArgument;
+  }
   if ((a.pos_out || a.pos_in || a.pos_of) && !grouped) {
     set_last_error("gemm_fp8_big: position-indexed rows need grouped mode");
     return kInvalidArgument;
   }
-  const int64_t out_rows = a.pos_out ? (int64_t)a.m_blocks * kBigBM : a.M;
+  const int64_t out_rows = a.pos_out ? (int64_t)a.m_blocks * bm : a.M;
   if (out_rows * a.ldc * 2 >= (int64_t)kOffNone || out_rows * a.inter >= (int64_t)kOffNone) {
     set_last_error("gemm_fp8_big: output larger than 4 GiB");
     return kUnsupported;
@@ -653,20 +692,13 @@ int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t st
     return kInvalidArgument;
   }
   // Row offsets are 32-bit byte offsets.
-  const int64_t a_rows = a.pos_in ? (int64_t)a.m_blocks * kBigBM
+  const int64_t a_rows = a.pos_in ? (int64_t)a.m_blocks * bm
                        : grouped ? (a.M + a.top_k - 1) / (a.top_k > 0 ? a.top_k : 1) : a.M;
   if (a_rows * a.lda >= ((int64_t)1 << 32) || (int64_t)a.N * a.ldb >= ((int64_t)1 << 32)) {
     set_last_error("gemm_fp8_big: operand larger than 4 GiB");
     return kUnsupported;
   }
-  if (grouped) {
-    if (epi == EPI_ACT) return run_big<EPI_ACT, true, true>(a, stream);
-    if (epi == EPI_STORE) return run_big<EPI_STORE, true, true>(a, stream);
-  } else if (epi == EPI_DENSE) {
-    return run_big<EPI_DENSE, false, false>(a, stream);
-  }
-  set_last_error("gemm_fp8_big: unsupported epilogue %d (grouped=%d)", epi, (int)grouped);
-  return kUnsupported;
+  return bm == 256 ? run_big_bm<256>(a, epi, grouped, stream) : run_big_bm<128>(a, epi, grouped, stream);
 }
 
 }  // namespace mstar

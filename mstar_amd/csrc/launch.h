@@ -141,12 +141,13 @@ int launch_stream_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dty
                        int max_rows, hipStream_t stream);
 bool stream_gemm_supported(int K, int max_rows, int akind, int bkind);
 
-// gemm_fp8.hip: 256 x 128 tile FP8 GEMM (8 waves, double-buffered LDS);
-// grouped needs the alignment block size 256.
 // W4A16 decode (router-ids mode): the CU-resident streaming kernel over
 // int4 weights (group-128 bf16 scales) and bf16 token rows.
 int launch_stream_int4_cu(const GemmArgs& a, int epi, hipStream_t stream);
-int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, hipStream_t stream);
+// gemm_fp8.hip: persistent FP8 GEMM over tiles of bm (256 or 128) token rows
+// x 256 weight rows (8 waves, double-buffered LDS); grouped, bm is the
+// alignment block size.
+int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, int bm, hipStream_t stream);
 // gemm_w4.hip: W4A16 grouped GEMM over alignment blocks of 64 tokens.  Token
 // rows (A) are stored in the int4 codes' pair order (each 8-group holds
 // elements 0, 4, 1, 5, 2, 6, 3, 7) with fp32 sums per 128-group (xs,

@@ -410,9 +410,9 @@ int launch_tile_gemm(const GemmArgs& a, int akind, int bkind, int epi, int dtype
     if (epi == EPI_STORE) return dispatch_bm<A_H16, B_INT4G, EPI_STORE, kBF16, true>(a, bm, stream);
     if (epi == EPI_ACT) return dispatch_bm<A_H16, B_INT4G, EPI_ACT, kBF16, true>(a, bm, stream);
   } else if (akind == A_FP8G && bkind == B_FP8BLK && grouped && dtype == kBF16 && bm == kBigBlockM) {
-    return launch_gemm_fp8_big(a, epi, true, stream);
+    return launch_gemm_fp8_big(a, epi, true, kBigBlockM, stream);
   } else if (akind == A_FP8R && bkind == B_FP8R && !grouped && dtype == kBF16 && bm == kBigBlockM) {
-    return launch_gemm_fp8_big(a, epi, false, stream);
+    return launch_gemm_fp8_big(a, epi, false, kBigBlockM, stream);
   } else if (akind == A_FP8G && bkind == B_FP8BLK && grouped && dtype == kBF16) {
     if (epi == EPI_STORE) return dispatch_bm<A_FP8G, B_FP8BLK, EPI_STORE, kBF16, true>(a, bm, stream);
     if (epi == EPI_ACT) return dispatch_bm<A_FP8G, B_FP8BLK, EPI_ACT, kBF16, true>(a, bm, stream);
