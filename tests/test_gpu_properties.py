@@ -1,7 +1,8 @@
 """Size-independent exact properties of the layer at BASELINE's full shapes
 (H=2048, E=128, top-8, I=768), for FP8 W8A8, W4A16 and bf16 weights: decode
-M=32 (the weight-streaming kernels) and prefill M=8192 with the Zipf bias
-(routing, alignment, the tile GEMMs, the top-k sum).  Every row of the output
+M=32 (the weight-streaming kernels), M=1024 (for FP8, the 128-row tile GEMM)
+and prefill M=8192 with the Zipf bias (routing, alignment, the tile GEMMs,
+the top-k sum).  Every row of the output
 is checked, bit for bit, with no tolerance:
 
 * routed weights times 2 -> output times 2: the routed weight enters only
@@ -82,7 +83,7 @@ QUANTS = ["fp8_w8a8", "w4a16", None]
 
 
 @pytest.mark.parametrize("quant", QUANTS, ids=["fp8", "w4a16", "bf16"])
-@pytest.mark.parametrize("M", [32, 8192])
+@pytest.mark.parametrize("M", [32, 1024, 8192])
 def test_routed_weight_scaling_is_exact(M, quant):
     x, tw, ti = _inputs(M, seed=M)
     print(f"properties: weight x2 M={M} {quant}", flush=True)
@@ -93,7 +94,7 @@ def test_routed_weight_scaling_is_exact(M, quant):
 
 
 @pytest.mark.parametrize("quant", QUANTS, ids=["fp8", "w4a16", "bf16"])
-@pytest.mark.parametrize("M", [32, 8192])
+@pytest.mark.parametrize("M", [32, 1024, 8192])
 def test_token_permutation_is_exact(M, quant):
     x, tw, ti = _inputs(M, seed=M + 1)
     perm = torch.randperm(M, generator=torch.Generator().manual_seed(M)).to(DEV)
@@ -104,7 +105,7 @@ def test_token_permutation_is_exact(M, quant):
 
 
 @pytest.mark.parametrize("quant", QUANTS, ids=["fp8", "w4a16", "bf16"])
-@pytest.mark.parametrize("M", [32, 8192])
+@pytest.mark.parametrize("M", [32, 1024, 8192])
 def test_expert_relabelling_is_exact(M, quant):
     x, tw, ti = _inputs(M, seed=M + 2)
     q1, s1, q2, s2 = _weights(quant)
