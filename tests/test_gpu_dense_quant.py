@@ -47,7 +47,7 @@ def _dense(M, N, K, seed):
 
 
 @pytest.mark.parametrize("M,N", [(32, 4096), (32, 2048), (100, 2048), (4096, 4096),
-                                 (65, 2048), (300, 1024)])  # 256-row blocks with all-padding waves
+                                 (65, 2048), (300, 1024)])  # row blocks with all-padding waves
 def test_fp8_scaled_mm_vs_oracle(M, N):
     from mstar_amd import ops
     K = 2048

@@ -424,8 +424,10 @@ def test_layer_under_hip_graph_replays():
 def test_moe_layer_from_logits(M, bias, quant):
     """Routing from logits + experts in one library call (mstar_moe_layer).
     Above 512 slots the multi-workgroup routing also quantises the hidden
-    rows; from M=384 (24 slots per expert) the 256-row FP8 tile kernel runs; W4A16 at M=1024 (Zipf
-    routing: experts spanning many 64-token blocks) runs the int4 tile GEMM."""
+    rows; from M=384 (24 slots per expert) the FP8 tile kernel runs, on 128-row
+    tiles below 128 slots per expert (M=512, 1024) and 256-row tiles above
+    (M=4096); W4A16 at M=1024 (Zipf routing: experts spanning many 64-token
+    blocks) runs the int4 tile GEMM."""
     from mstar_amd import _lib, ops, quant as Q
     H, E, I, k = 2048, 128, 768, 8
     x = _hidden(M, H, seed=M + 21)
