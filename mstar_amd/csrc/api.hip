@@ -73,6 +73,10 @@ struct Plan {
   // reduced, the down output) are stored by sorted position, so every tile
   // reads and writes contiguous rows; the top-k sum gathers through pos_of.
   bool by_pos = false;
+  // FP8 decode layer: gate_up and down in one streaming launch
+  // (launch_stream_fp8_layer), synchronised per expert through off_sync,
+  // which the routing launch clears.
+  bool one_launch = false;
   // W4A16 above decode size: the 64-token int4 tile GEMM (gemm_w4.hip).
   bool w4_tile = false;
   // FP8 on the persistent tile GEMM (gemm_fp8.hip), bm = 256 or 128 rows.
@@ -80,7 +84,7 @@ struct Plan {
   int bm = 16;
   int64_t slots = 0, max_padded = 0, max_blocks = 0;
   size_t off_sorted, off_eids, off_ntpp, off_eoff, off_ecnt, off_c2, off_c3, off_hq, off_hs,
-      off_cq, off_cs, off_scratch, scratch_bytes, off_tw, off_ids, off_pos, off_w4h, off_w4hx, off_w4cx, total;
+      off_cq, off_cs, off_scratch, scratch_bytes, off_tw, off_ids, off_pos, off_w4h, off_w4hx, off_w4cx, off_sync, total;
 };
 
 // with_route: the plan also holds the router outputs and the routing scratch
@@ -141,6 +145,8 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->route_quant = with_route && ((pl->ids_mode && quant == MSTAR_QUANT_FP8_W8A8 && H % 512 == 0) ||
                                    (quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream &&
                                     route_is_grid(M, top_k)));
+  pl->one_launch = pl->route_quant && pl->stream && reduce && stream_fp8_layer_supported(H, I, pl->slots, E);
+  pl->off_sync = pl->one_launch ? take((size_t)(E + 1) * 4) : 0;
   pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;
   pl->off_hs = fp8_tiled || pl->route_quant ? take((size_t)M * (H / 128) * 4) : 0;
   const size_t cq_rows = pl->by_pos ? pos_rows : (size_t)pl->slots;
@@ -231,9 +237,13 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
       g1.A = ws + pl.off_hq; g1.a_scale = (const float*)(ws + pl.off_hs); g1.ld_as = H / 128;
       g1.a_q16 = 1;
     }
-    st = launch_stream_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, (int)M, stream);
-    if (st != kOk) return st;
-    st = launch_stream_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, (int)M, stream);
+    if (pl.one_launch) {
+      st = launch_stream_fp8_layer(g1, g2, (int*)(ws + pl.off_sync), stream);
+    } else {
+      st = launch_stream_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, (int)M, stream);
+      if (st != kOk) return st;
+      st = launch_stream_gemm(g2, A_H16, bkind, EPI_STORE, act_dtype, (int)M, stream);
+    }
     if (st != kOk) return st;
   } else if (bkind == B_FP8BLK) {
     uint8_t* hq = ws + pl.off_hq;
@@ -614,7 +624,9 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
     st = launch_topk_softmax(router_logits, logits_dtype, num_tokens, num_experts, top_k,
                              renormalize, tw, ids32, topk_ids_out, stream,
                              pl.route_quant ? hidden : nullptr, hidden_size,
-                             (uint16_t*)(ws + pl.off_hq), (float*)(ws + pl.off_hs));
+                             (uint16_t*)(ws + pl.off_hq), (float*)(ws + pl.off_hs),
+                             pl.one_launch ? (int*)(ws + pl.off_sync) : nullptr,
+                             pl.one_launch ? num_experts + 1 : 0);
   else
     st = launch_route(router_logits, logits_dtype, num_tokens, num_experts, top_k, renormalize, tw,
                       ids32, topk_ids_out, pl.bm, (int32_t*)(ws + pl.off_sorted),
@@ -647,6 +659,7 @@ int mstar_moe_block(const void* hidden, int act_dtype, int64_t num_tokens, int64
   // The router launch does not quantise the hidden rows: the experts read
   // (and, where needed, quantise) them as mstar_fused_moe does.
   pl.route_quant = false;
+  pl.one_launch = false;  // nothing clears the sync words before the experts
   if ((st = check_layer_args(pl, activation, workspace, workspace_bytes)) != kOk) return st;
   if (num_tokens == 0) return kOk;
   if (!hidden || !gate_weight || !w1 || !w2 || !out ||

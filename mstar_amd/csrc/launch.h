@@ -27,10 +27,11 @@ int occupancy_per_cu(const void* kernel, int threads, size_t lds_bytes);
 int launch_router(const void* hidden, int64_t M, int64_t H, const void* gate_weight, int E, int k,
                   int renorm, float* w, int32_t* ids32, int64_t* ids64, void* logits_out,
                   hipStream_t stream);
+// zero / n_zero: words the launch clears (for the launch after it).
 int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, int k,
                         int renorm, float* w, int32_t* ids32, int64_t* ids64, hipStream_t stream,
                         const void* hidden = nullptr, int64_t H = 0, uint16_t* hq = nullptr,
-                        float* hs = nullptr);
+                        float* hs = nullptr, int* zero = nullptr, int n_zero = 0);
 // Alignment: one workgroup for numel <= 4096 (or without scratch), otherwise
 // a histogram pass and a scan+scatter pass over align_scratch_bytes() of
 // scratch.  Deterministic (slots ascend within an expert) either way.
@@ -171,6 +172,12 @@ constexpr int kBigBlockM = 256;
 // otherwise with the FP8 MFMA.
 int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream);
 constexpr int64_t kStreamMaxIdsSlots = 1024;  // slots a launch in ids mode can take
+// The FP8 decode layer's gate_up and down streaming GEMMs in one launch
+// (g1: gate_up on the routing launch's widened FP8 token rows; g2: down on
+// g1's bf16 output).  sync_words: E + 1 ints, zero when the launch starts
+// (the routing launch clears them).
+bool stream_fp8_layer_supported(int64_t H, int64_t I, int64_t slots, int E);
+int launch_stream_fp8_layer(const GemmArgs& g1, const GemmArgs& g2, int* sync_words, hipStream_t stream);
 bool stream_fp8_supported(int K, int N, int inter, int epi);
 
 

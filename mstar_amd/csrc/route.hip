@@ -30,8 +30,11 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict_
                                                            int64_t* __restrict__ ids64,
                                                            const uint16_t* __restrict__ hidden,
                                                            int64_t H, uint16_t* __restrict__ hq,
-                                                           float* __restrict__ hs) {
+                                                           float* __restrict__ hs, int* __restrict__ zero,
+                                                           int n_zero) {
   const int lane = threadIdx.x & 63;
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < n_zero; i += blockDim.x) zero[i] = 0;
   // With `hidden`, two waves per token: the even one routes, the odd one
   // quantises the hidden row, in parallel.
   const int wpt = hidden ? 2 : 1;
@@ -443,7 +446,7 @@ __global__ __launch_bounds__(kAlignThreads) void scatter_kernel(
 int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, int k,
                         int renorm, float* w, int32_t* ids32, int64_t* ids64,
                         hipStream_t stream, const void* hidden, int64_t H, uint16_t* hq,
-                        float* hs) {
+                        float* hs, int* zero, int n_zero) {
   if (hidden && (H <= 0 || H % 512 != 0 || !hq || !hs)) {
     set_last_error("topk_softmax: hidden quantisation needs H %% 512 == 0 (H=%lld)", (long long)H);
     return kInvalidArgument;
@@ -470,15 +473,15 @@ int launch_topk_softmax(const void* logits, int logits_dtype, int64_t M, int E, 
     if (logits_dtype == kF32)                                                                \
       topk_softmax_kernel<float, N><<<grid, block, 0, stream>>>(                             \
           (const float*)logits, M, E, k, renorm, w, ids32, ids64, (const uint16_t*)hidden, H, \
-          hq, hs);                                                                           \
+          hq, hs, zero, n_zero);                                                        \
     else if (logits_dtype == kF16)                                                           \
       topk_softmax_kernel<_Float16, N><<<grid, block, 0, stream>>>(                          \
           (const _Float16*)logits, M, E, k, renorm, w, ids32, ids64, (const uint16_t*)hidden, \
-          H, hq, hs);                                                                        \
+          H, hq, hs, zero, n_zero);                                                     \
     else                                                                                     \
       topk_softmax_kernel<uint16_t, N><<<grid, block, 0, stream>>>(                          \
           (const uint16_t*)logits, M, E, k, renorm, w, ids32, ids64, (const uint16_t*)hidden, \
-          H, hq, hs);                                                                        \
+          H, hq, hs, zero, n_zero);                                                     \
     break;
   // Experts per lane, rounded up to a power of two (E <= 1024).
   const int epl2 = epl <= 1 ? 1 : epl <= 2 ? 2 : epl <= 4 ? 4 : epl <= 8 ? 8 : 16;

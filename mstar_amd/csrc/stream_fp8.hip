@@ -429,9 +429,52 @@ __device__ __forceinline__ void wait_leaving_chunks(int ahead) {
 // the 16 rows' reads of one logical piece fall in distinct banks.
 __device__ __forceinline__ int w4_swz(int r) { return (r >> 1) & 7; }
 
-template <int EPI, int KS, int STAGE>
-__global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void stream_fp8_cu_kernel(
-    GemmArgs p, int cap) {
+// 16 bytes of 16-bit row data; COHERENT: as two agent-scope atomic loads,
+// which see other XCDs' agent-scope atomic stores without an L2 invalidate.
+template <bool COHERENT>
+__device__ __forceinline__ v4i load_rows16(const uint16_t* p) {
+  if constexpr (COHERENT) {
+    const uint64_t lo = __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t hi = __hip_atomic_load((const uint64_t*)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return v4i{(int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi, (int)(uint32_t)(hi >> 32)};
+  } else {
+    return *(const v4i*)p;
+  }
+}
+
+// Phase timestamps of the streaming kernels (a timeline build only:
+// compiled with MSTAR_TIMELINE, read back with mstar_debug_timeline).
+#ifdef MSTAR_TIMELINE
+__device__ uint64_t g_timeline[2 * 1024 * 8];  // [EPI][workgroup][phase]
+#define MSTAR_TL(i)                                                                          \
+  do {                                                                                       \
+    if (threadIdx.x == 0) g_timeline[((EPI & 1) * 1024 + blockIdx.x) * 8 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define MSTAR_TL(i) \
+  do {              \
+  } while (0)
+#endif
+
+// The decode layer in one launch (stream_fp8_layer_kernel): the gate_up
+// phase of a workgroup reports, per expert, the (item, token row) pairs it
+// finished; the down phase stages an expert's activation rows only once
+// all of that expert's gate_up pairs are reported.
+enum : int { kPhaseAlone = 0, kPhaseGate = 1, kPhaseDown = 2 };
+struct LayerSync {
+  int* done;       // [E] gate_up (item, token row) pairs finished per expert; zero at launch
+  int* err;        // set to 1 if a wait gave up (output of that launch invalid)
+  int gate_ipe;    // gate_up items per expert (inter / 8)
+};
+// Longest wait of the down phase for an expert's gate_up rows before it
+// gives up (s_memrealtime ticks of 10 ns): 20 ms.
+constexpr uint64_t kLayerWaitTicks = 2000000;
+
+// One workgroup's share of a streaming GEMM: work range `wg` of `nwg`.
+template <int EPI, int KS, int STAGE, int PHASE = kPhaseAlone>
+__device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int wg, int nwg, const LayerSync& ls) {
+  static_assert(PHASE == kPhaseAlone || (STAGE != STAGE_W4 && (PHASE == kPhaseGate) == (EPI == EPI_ACT)),
+                "layer phases: FP8 gate_up, then FP8 down");
   constexpr bool W4 = STAGE == STAGE_W4;
   static_assert(!W4 || KS % 2 == 0, "int4 chunks are two K-steps");
   constexpr int PITCH = cu_pitch<KS>();
@@ -470,9 +513,11 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
   uint16_t* C = (uint16_t*)p.C;
   uint8_t* ring = smem + w * WAVE_RING;
 
+  MSTAR_TL(0);
   // ---- prologue 1: per-expert counts and the active-expert mask.
   for (int e = tid; e < E; e += NTH) sCnt[e] = 0;
   if (tid < 32) sMask[tid] = 0;
+  MSTAR_TL(1);
   lds_sync();
   int my_e[SPT], my_pos[SPT];
 #pragma unroll
@@ -493,12 +538,13 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
   }
   lds_sync();
   // Active experts: prefix popcounts of the mask words (lane i: word i).
+  MSTAR_TL(2);
   const uint32_t mword = lane < 32 ? sMask[lane] : 0u;
   const int wincl = wave_incl_scan(__builtin_popcount(mword));
   const int n_act = wave_last(wincl);
   const int total = n_act * IPE;
-  const int T = (total + gridDim.x - 1) / gridDim.x;
-  const int i0 = blockIdx.x * T;
+  const int T = (total + nwg - 1) / nwg;
+  const int i0 = wg * T;
   const int i1 = i0 + T < total ? i0 + T : total;
   if (i0 >= i1) return;
   auto active_expert = [&](int a) -> int {  // the a-th active expert (wave-uniform a)
@@ -614,6 +660,7 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
     if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * NTH;
   lds_sync();
   const int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
+  MSTAR_TL(3);
 
   // ---- staging (waves < SW): `nrows` rows; row j reads A row arow_of(j).
   // The staging waves hold no prefetched weights, so their loads are all in
@@ -664,7 +711,7 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
         const int gq = g0 + j * (ST / 16) + (tid >> 4), sub = tid & 15;
         const bool live = gq < groups;
         const int r = live ? gq / KS : 0, ks = live ? gq - (gq / KS) * KS : 0;
-        raw[j] = live ? *(const v4i*)(A16 + (int64_t)arow_of(r) * p.lda + ks * 128 + sub * 8)
+        raw[j] = live ? load_rows16<PHASE == kPhaseDown>(A16 + (int64_t)arow_of(r) * p.lda + ks * 128 + sub * 8)
                       : v4i{0, 0, 0, 0};
       }
 #pragma unroll
@@ -920,7 +967,12 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
                 }
                 pk[h] = two;
               }
-              *(uint2*)(C + (int64_t)slot_id * p.ldc + g * 8 + 4 * lg) = make_uint2(pk[0], pk[1]);
+              uint16_t* dst = C + (int64_t)slot_id * p.ldc + g * 8 + 4 * lg;
+              if constexpr (PHASE == kPhaseGate)  // read by other XCDs' down phases
+                __hip_atomic_store((uint64_t*)dst, (uint64_t)pk[0] | ((uint64_t)pk[1] << 32), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+              else
+                *(uint2*)dst = make_uint2(pk[0], pk[1]);
             }
           } else {
             if (tok_ok) {
@@ -967,6 +1019,27 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
     const int lbase = sOff[sAct[wa0]] + wr0;  // list index of staged row 0
     if (!first_window) lds_sync();             // every wave is done with the previous window
     first_window = false;
+    if constexpr (PHASE == kPhaseDown) {
+      // Wait until the gate_up phases reported every row of the window's
+      // experts (one wave polls, a lane per expert, about once a
+      // microsecond: every poll is a memory request that competes with the
+      // weight streams), then the staging waves acquire their stores.
+      if (w == 0) {
+        for (int aa = wa0 + lane; aa <= wa1; aa += 64) {
+          const int e = sAct[aa];
+          const int target = ls.gate_ipe * sCnt[e];
+          const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+          while (__hip_atomic_load(ls.done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kLayerWaitTicks) {
+              __hip_atomic_store(ls.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(32);
+          }
+        }
+      }
+      lds_sync();  // the staging reads the rows as agent-scope atomics (load_rows16)
+    }
     if (w < SW) {
       const auto arow_of = [&](int j) { return sList[lbase + j] / p.top_k; };
       if constexpr (STAGE == STAGE_Q16) stage_copy_q16(nrows, arow_of);
@@ -977,9 +1050,60 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
           sRw[j] = load_weight_any(p.topk_w, p.topk_w_dtype, sList[lbase + j]);
     }
     lds_sync();
+    MSTAR_TL(4);
     run_window(lbase);
+    MSTAR_TL(5);
   }
   wait_vmcnt<0>();  // no DMA outlives the kernel
+  MSTAR_TL(7);
+  if constexpr (PHASE == kPhaseGate) {
+    // Report this range's (item, row) pairs per expert once every wave's
+    // stores are complete (the wait above): one lane per expert adds
+    // (items of the expert in [i0, i1)) x (its rows).  The activation rows
+    // were stored as agent-scope atomics, which are coherent across XCDs
+    // without the L2 write-back an agent-scope release fence costs.
+    lds_sync();
+    if (w == 0) {
+      for (int a = a_first + lane; a <= a_last; a += 64) {
+        const int lo = i0 > a * IPE ? i0 : a * IPE;
+        const int hi = i1 < (a + 1) * IPE ? i1 : (a + 1) * IPE;
+        const int e = sAct[a];
+        __hip_atomic_fetch_add(ls.done + e, (hi - lo) * sCnt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+template <int EPI, int KS, int STAGE>
+__global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void stream_fp8_cu_kernel(
+    GemmArgs p, int cap) {
+  stream_cu_body<EPI, KS, STAGE>(p, cap, blockIdx.x, gridDim.x, LayerSync{});
+}
+
+// Range of workgroup b: consecutive ranges go to workgroups of one XCD
+// (workgroups are dealt to the 8 XCDs round-robin), so the gate_up ranges
+// an expert's down work waits on ran on the same XCD.
+#ifndef MSTAR_XCD_MAP
+#define MSTAR_XCD_MAP 1
+#endif
+__device__ __forceinline__ int xcd_range(int b, int nwg) {
+  return MSTAR_XCD_MAP && nwg % 8 == 0 ? (b % 8) * (nwg / 8) + b / 8 : b;
+}
+
+// The FP8 decode layer's two streaming GEMMs in one launch: each workgroup
+// runs its gate_up range (bf16-widened FP8 token rows from the routing
+// launch -> bf16 SiLU-and-mul rows), then its down range, staging an
+// expert's rows once the gate_up phases that cover the expert reported
+// them (LayerSync).  Every workgroup's gate_up phase runs without waiting,
+// so the waits end as long as the workgroups a wait depends on are
+// resident; a wait that passes kLayerWaitTicks sets ls.err and goes on.
+template <int KS1, int KS2>
+__global__ __launch_bounds__(kCuThreads) void stream_fp8_layer_kernel(GemmArgs g1, GemmArgs g2, int cap1, int cap2,
+                                                                      LayerSync ls) {
+  const int r = xcd_range(blockIdx.x, gridDim.x);
+  stream_cu_body<EPI_ACT, KS1, STAGE_Q16, kPhaseGate>(g1, cap1, r, gridDim.x, ls);
+  __syncthreads();  // every wave is done with the gate_up phase's LDS
+  stream_cu_body<EPI_STORE, KS2, STAGE_H16, kPhaseDown>(g2, cap2, r, gridDim.x, ls);
 }
 
 
@@ -1041,6 +1165,53 @@ static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, in
     *status = epi == EPI_ACT ? run_stream_fp8_cu<EPI_ACT, KS, STAGE_H16>(a, cap, shmem, stream)
                              : run_stream_fp8_cu<EPI_STORE, KS, STAGE_H16>(a, cap, shmem, stream);
   return true;
+}
+
+// Rows a window of the CU-resident FP8 kernel stages, and its dynamic LDS.
+template <int KS>
+static bool cu_window(const GemmArgs& a, int* cap_out, size_t* shmem_out) {
+  const size_t per_row = (size_t)cu_pitch<KS>() + (KS + 1) * 4;
+  const size_t fixed = cu_sc_off<KS>(a.num_experts, a.M) + 16 + 1024;
+  if (fixed + 4 * per_row > kCuLdsMax) return false;
+  int cap = (int)((kCuLdsMax - fixed) / per_row);
+  if (cap > 1024) cap = 1024;
+  *cap_out = cap;
+  *shmem_out = cu_rows_off<KS>(a.num_experts, a.M, cap) + (size_t)cap * cu_pitch<KS>();
+  return true;
+}
+
+template <int KS1, int KS2>
+static int run_stream_fp8_layer(const GemmArgs& g1, const GemmArgs& g2, const LayerSync& ls,
+                                hipStream_t stream) {
+  int cap1, cap2;
+  size_t sh1, sh2;
+  if (!cu_window<KS1>(g1, &cap1, &sh1) || !cu_window<KS2>(g2, &cap2, &sh2)) {
+    set_last_error("stream_fp8_layer: the windows do not fit in LDS");
+    return kUnsupported;
+  }
+  const size_t shmem = sh1 > sh2 ? sh1 : sh2;
+  auto kern = stream_fp8_layer_kernel<KS1, KS2>;
+  const int st = ensure_dynamic_lds((const void*)kern, shmem, "stream_fp8_layer");
+  if (st != kOk) return st;
+  kern<<<dim3(device_cu_count()), dim3(kCuThreads), shmem, stream>>>(g1, g2, cap1, cap2, ls);
+  return launch_status("stream_fp8_layer");
+}
+
+bool stream_fp8_layer_supported(int64_t H, int64_t I, int64_t slots, int E) {
+  return H == 2048 && I == 768 && slots <= kStreamMaxIdsSlots && E <= 1024;
+}
+
+int launch_stream_fp8_layer(const GemmArgs& g1, const GemmArgs& g2, int* sync_words, hipStream_t stream) {
+  if (!stream_fp8_layer_supported(g1.K, g1.inter, g1.M, g1.num_experts) || !g1.topk_ids || !g2.topk_ids ||
+      !g1.a_q16 || !g1.a_scale || g2.a_scale || g2.K != g1.inter || g2.N != g1.K || !sync_words) {
+    set_last_error("stream_fp8_layer: unsupported configuration");
+    return kUnsupported;
+  }
+  LayerSync ls;
+  ls.done = sync_words;
+  ls.err = sync_words + g1.num_experts;
+  ls.gate_ipe = g1.inter / 8;
+  return run_stream_fp8_layer<16, 6>(g1, g2, ls, stream);
 }
 
 int launch_stream_int4_cu(const GemmArgs& a, int epi, hipStream_t stream) {
@@ -1133,3 +1304,9 @@ int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream
 }
 
 }  // namespace mstar
+
+#ifdef MSTAR_TIMELINE
+extern "C" int mstar_debug_timeline(uint64_t* dst, size_t n) {
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(mstar::g_timeline), n * 8, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 1;
+}
+#endif
