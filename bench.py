@@ -422,7 +422,6 @@ def main():
         g, _ = capture(lambda w=w: layer(x, logits, w))
         graphs.append(g)
     single_us = time_graphs(graphs, args.steps, args.warmup) * 1e6
-    del graphs
     hits = n_hit(logits)
     layer_bytes = hits * (EXPERT_FP8_BYTES + EXPERT_SCALE_BYTES) + M * H * 3 + M * (H // 128) * 4 + M * E * 4
     layer_gbs = layer_bytes / sec / 1e9
@@ -491,7 +490,7 @@ def main():
             out["prefill"]["library_reference"] = prefill_library_reference(P)
 
     if not args.no_extra:
-        del weights, graphs
+        del weights, graphs, gmulti
         torch.cuda.empty_cache()
         out["dense_fp8"] = dense_fp8_lines(args)
         out["w4a16"] = w4a16_lines(args)

@@ -33,8 +33,7 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const LT* __restrict_
                                                            float* __restrict__ hs, int* __restrict__ zero,
                                                            int n_zero) {
   const int lane = threadIdx.x & 63;
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < n_zero; i += blockDim.x) zero[i] = 0;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_zero; i += gridDim.x * blockDim.x) zero[i] = 0;
   // With `hidden`, two waves per token: the even one routes, the odd one
   // quantises the hidden row, in parallel.
   const int wpt = hidden ? 2 : 1;

@@ -394,10 +394,12 @@ template <int KS, bool W4 = false>
 __host__ __device__ constexpr size_t cu_ring_bytes() {
   return (size_t)cu_waves<W4>() * kCuRing * (W4 ? cu_w4_slot<KS>() : cu_kc<KS>() * 2048);
 }
-// LDS layout: rings | sAct[E] sCnt[E] sOff[E] sList[M'] | sSc[cap][KS] sRw[cap] |
-// rows[cap][pitch]
+// LDS layout: rings | sAct[E] sCnt[E] sOff[E] sList[M'] sMask[32] | sSc[cap][KS]
+// sRw[cap] | rows[cap][pitch].  The lists sit at the same offset for every KS
+// with the same ring size, so the layout kernel's down phase reuses the
+// gate_up phase's lists.
 __host__ __device__ inline size_t cu_lists_bytes(int E, int64_t M) {
-  return ((size_t)3 * E + (size_t)((M + 3) & ~3ll)) * 4;
+  return ((size_t)3 * E + (size_t)((M + 3) & ~3ll) + 32) * 4;
 }
 template <int KS, bool W4 = false>
 __host__ __device__ inline size_t cu_sc_off(int E, int64_t M) {
@@ -504,7 +506,10 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
   float* sSc = (float*)(smem + cu_sc_off<KS, W4>(E, p.M));
   float* sRw = sSc + cap * KS;  // routed weight of each staged row
   uint8_t* sRows = smem + cu_rows_off<KS, W4>(E, p.M, cap);
-  __shared__ uint32_t sMask[32];  // active experts (E <= 1024)
+  uint32_t* sMask = (uint32_t*)(sList + ((p.M + 3) & ~3ll));  // [32] active experts (E <= 1024)
+  // The down phase of the layer kernel finds the lists the gate_up phase
+  // built from the same router ids.
+  constexpr bool kListsBuilt = PHASE == kPhaseDown;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
@@ -515,28 +520,30 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
 
   MSTAR_TL(0);
   // ---- prologue 1: per-expert counts and the active-expert mask.
-  for (int e = tid; e < E; e += NTH) sCnt[e] = 0;
-  if (tid < 32) sMask[tid] = 0;
-  MSTAR_TL(1);
-  lds_sync();
   int my_e[SPT], my_pos[SPT];
+  if constexpr (!kListsBuilt) {
+    for (int e = tid; e < E; e += NTH) sCnt[e] = 0;
+    if (tid < 32) sMask[tid] = 0;
+    MSTAR_TL(1);
+    lds_sync();
 #pragma unroll
-  for (int j = 0; j < SPT; ++j) {
-    const int i = tid + j * NTH;
-    int e = -1;
-    if (i < p.M) {
-      const int64_t v = p.ids_dtype == kI64 ? ((const int64_t*)p.topk_ids)[i]
-                                            : (int64_t)((const int32_t*)p.topk_ids)[i];
-      e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are skipped (.cu:44-46)
+    for (int j = 0; j < SPT; ++j) {
+      const int i = tid + j * NTH;
+      int e = -1;
+      if (i < p.M) {
+        const int64_t v = p.ids_dtype == kI64 ? ((const int64_t*)p.topk_ids)[i]
+                                              : (int64_t)((const int32_t*)p.topk_ids)[i];
+        e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are skipped (.cu:44-46)
+      }
+      my_e[j] = e;
+      my_pos[j] = 0;
+      if (e >= 0) {
+        my_pos[j] = atomicAdd(&sCnt[e], 1);
+        atomicOr(&sMask[e >> 5], 1u << (e & 31));
+      }
     }
-    my_e[j] = e;
-    my_pos[j] = 0;
-    if (e >= 0) {
-      my_pos[j] = atomicAdd(&sCnt[e], 1);
-      atomicOr(&sMask[e >> 5], 1u << (e & 31));
-    }
+    lds_sync();
   }
-  lds_sync();
   // Active experts: prefix popcounts of the mask words (lane i: word i).
   MSTAR_TL(2);
   const uint32_t mword = lane < 32 ? sMask[lane] : 0u;
@@ -546,7 +553,9 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
   const int T = (total + nwg - 1) / nwg;
   const int i0 = wg * T;
   const int i1 = i0 + T < total ? i0 + T : total;
-  if (i0 >= i1) return;
+  // Without work a workgroup is done, except that the gate_up phase of the
+  // layer kernel still builds the lists for its down phase.
+  if (i0 >= i1 && PHASE != kPhaseGate) return;
   auto active_expert = [&](int a) -> int {  // the a-th active expert (wave-uniform a)
     const uint64_t past = __ballot(wincl > a);
     const int word = __builtin_ctzll(past);
@@ -636,29 +645,32 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
   }
 
   // ---- prologue 2: offsets, active list, slot lists.
-  if (w == 0) {
-    int run = 0;
-    for (int e0 = 0; e0 < E; e0 += 64) {
-      const int e = e0 + lane;
-      const int c = e < E ? sCnt[e] : 0;
-      const int incl = wave_incl_scan(c);
-      if (e < E) sOff[e] = run + incl - c;
-      run += wave_last(incl);
+  if constexpr (!kListsBuilt) {
+    if (w == 0) {
+      int run = 0;
+      for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const int c = e < E ? sCnt[e] : 0;
+        const int incl = wave_incl_scan(c);
+        if (e < E) sOff[e] = run + incl - c;
+        run += wave_last(incl);
+      }
+      int n = 0;
+      for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const bool act = e < E && sCnt[e] > 0;
+        const uint64_t b = __ballot(act);
+        if (act) sAct[n + __builtin_popcountll(b & ((1ull << lane) - 1ull))] = e;
+        n += __builtin_popcountll(b);
+      }
     }
-    int n = 0;
-    for (int e0 = 0; e0 < E; e0 += 64) {
-      const int e = e0 + lane;
-      const bool act = e < E && sCnt[e] > 0;
-      const uint64_t b = __ballot(act);
-      if (act) sAct[n + __builtin_popcountll(b & ((1ull << lane) - 1ull))] = e;
-      n += __builtin_popcountll(b);
-    }
-  }
-  lds_sync();
+    lds_sync();
 #pragma unroll
-  for (int j = 0; j < SPT; ++j)
-    if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * NTH;
-  lds_sync();
+    for (int j = 0; j < SPT; ++j)
+      if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * NTH;
+    lds_sync();
+  }
+  if (PHASE == kPhaseGate && i0 >= i1) return;
   const int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
   MSTAR_TL(3);
 
@@ -1083,11 +1095,8 @@ __global__ __launch_bounds__(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads) void
 // Range of workgroup b: consecutive ranges go to workgroups of one XCD
 // (workgroups are dealt to the 8 XCDs round-robin), so the gate_up ranges
 // an expert's down work waits on ran on the same XCD.
-#ifndef MSTAR_XCD_MAP
-#define MSTAR_XCD_MAP 1
-#endif
 __device__ __forceinline__ int xcd_range(int b, int nwg) {
-  return MSTAR_XCD_MAP && nwg % 8 == 0 ? (b % 8) * (nwg / 8) + b / 8 : b;
+  return nwg % 8 == 0 ? (b % 8) * (nwg / 8) + b / 8 : b;
 }
 
 // The FP8 decode layer's two streaming GEMMs in one launch: each workgroup
