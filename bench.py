@@ -54,14 +54,15 @@ EXPERT_FP8_BYTES = 2 * INTER * H + H * INTER                      # 4,718,592
 EXPERT_SCALE_BYTES = ((2 * INTER // 128) * (H // 128) + (H // 128) * (INTER // 128)) * 4  # 1,152
 W_COPIES = 4
 COPY_BYTES = 512 << 20
-# HBM traffic of one gate_up launch at config 2 (seed 0, 115 hit experts),
-# from two rocprofv3 --pmc passes over `bench.py --kernel-only` (FETCH_SIZE,
-# then WRITE_SIZE; KiB per dispatch, mean of 24 dispatches).  Each counter
-# is scaled by what it reads for torch's neg kernel over COPY_BYTES in the
-# same run: FETCH_SIZE reports 262,150.6 KiB for the 524,288 KiB read
-# (x2.0), WRITE_SIZE 524,288 KiB for the 524,288 KiB written (x1.0).
-GATE_UP_FETCH_KIB, FETCH_FACTOR = 177354.4, 2.0
-GATE_UP_WRITE_KIB, WRITE_FACTOR = 386.4, 1.0
+# HBM traffic of one layer-kernel launch at config 2 (seed 0, 115 hit
+# experts), from two rocprofv3 --pmc passes over `bench.py --kernel-only`
+# (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch, mean over the dispatches).
+# Each counter is scaled by what it reads for torch's neg kernel over
+# COPY_BYTES in the same run: FETCH_SIZE reports 262,153.5 KiB for the
+# 524,288 KiB read (x2.0), WRITE_SIZE 524,288 KiB for the 524,288 KiB
+# written (x1.0).
+LAYER_FETCH_KIB, FETCH_FACTOR = 265877.8, 2.0
+LAYER_WRITE_KIB, WRITE_FACTOR = 1801.8, 1.0
 
 
 def parse():
@@ -78,7 +79,7 @@ def parse():
     p.add_argument("--no-sweep", action="store_true",
                    help="skip the prefill M=512/2048 and dense N=4096/2048 lines (profiler runs)")
     p.add_argument("--kernel-only", action="store_true",
-                   help="launch only the gate_up GEMM in a loop (for profiler runs)")
+                   help="launch only the layer's expert kernel in a loop (for profiler runs)")
     p.add_argument("--profile-prefill", action="store_true",
                    help="run the config-3 prefill layer eagerly --steps times, no graphs "
                         "(for rocprofv3 --pmc runs, which count per dispatch)")
@@ -165,41 +166,53 @@ def n_hit(logits):
     return int(torch.unique(ti).numel())
 
 
-def gate_up_kernel_timing(x, logits, weights, steps, warmup):
-    """Mean duration of the layer's gate_up GEMM alone (the kernel the decode
-    layer runs: weight streaming driven by the router ids, activations
-    quantised by the routing launch), from HIP events recorded on the stream
-    the kernel is launched on."""
+def layer_kernel_bytes(M, hits):
+    """Algorithmic HBM bytes of one launch of the layer kernel (gate_up + down):
+    every hit expert's FP8 weights and block scales once, the widened FP8
+    token rows and their scales in, the SiLU-and-mul rows out and back in,
+    the down rows (x routed weight) out, the router ids and weights in."""
+    slots = M * K_TOP
+    return (hits * (EXPERT_FP8_BYTES + EXPERT_SCALE_BYTES) + M * H * 2 + M * (H // 128) * 4
+            + 2 * slots * INTER * 2 + slots * H * 2 + slots * 8)
+
+
+def layer_kernel_timing(x, logits, weights, steps, warmup):
+    """Mean duration of the decode layer's expert launch alone (gate_up and
+    down in one kernel, mstar_moe_stream_layer) on the routing launch's
+    outputs, from HIP events recorded on the stream the kernel is launched on.
+    Every launch gets its own zeroed sync words (allocated before timing)."""
     from mstar_amd import _lib
     lib = _lib.load()
     M = x.shape[0]
     dev = x.device
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
-    tw = torch.empty(M, K_TOP, dtype=torch.float32, device=dev)
-    ti = torch.empty(M, K_TOP, dtype=torch.int32, device=dev)
+    slots = M * K_TOP
+    tw = torch.empty(slots, dtype=torch.float32, device=dev)
+    ti = torch.empty(slots, dtype=torch.int32, device=dev)
     hq = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
     hs = torch.empty(M, H // 128, dtype=torch.float32, device=dev)
     _lib.check(lib.mstar_moe_topk_softmax_quant(
         logits.data_ptr(), _lib.DT_F32, M, E, K_TOP, 1, tw.data_ptr(), ti.data_ptr(), None,
         x.data_ptr(), H, hq.data_ptr(), hs.data_ptr(), sp), "topk_softmax_quant")
-    slots = M * K_TOP
-    c2 = torch.empty(slots, INTER, dtype=torch.bfloat16, device=dev)
+    act = torch.empty(slots, INTER, dtype=torch.bfloat16, device=dev)
+    rows = torch.empty(slots, H, dtype=torch.bfloat16, device=dev)
+    sync = torch.zeros(warmup + steps, E + 1, dtype=torch.int32, device=dev)
 
-    def launch(w):
-        q1, s1, _, _ = w
-        _lib.check(lib.mstar_moe_stream_gemm(
-            hq.data_ptr(), _lib.DT_FP8_AS_BF16, hs.data_ptr(), q1.data_ptr(), s1.data_ptr(),
-            c2.data_ptr(), tw.data_ptr(), _lib.DT_F32, ti.data_ptr(), _lib.DT_I32, slots, E,
-            2 * INTER, H, K_TOP, 0, 0, sp), "moe_stream_gemm")
+    def launch(i, w):
+        q1, s1, q2, s2 = w
+        _lib.check(lib.mstar_moe_stream_layer(
+            hq.data_ptr(), hs.data_ptr(), q1.data_ptr(), s1.data_ptr(), q2.data_ptr(), s2.data_ptr(),
+            tw.data_ptr(), ti.data_ptr(), M, H, E, INTER, K_TOP, 0, act.data_ptr(), rows.data_ptr(),
+            sync[i].data_ptr(), sp), "moe_stream_layer")
 
     for i in range(warmup):
-        launch(weights[i % len(weights)])
+        launch(i, weights[i % len(weights)])
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
     for i in range(steps):
-        launch(weights[i % len(weights)])
+        launch(warmup + i, weights[i % len(weights)])
     end.record(stream)
     end.synchronize()
     return start.elapsed_time(end) * 1e3 / steps  # us
@@ -401,8 +414,8 @@ def main():
         dst = torch.empty_like(src)
         torch.neg(src, out=dst)
         torch.cuda.synchronize()
-        us = gate_up_kernel_timing(x, logits, weights, args.steps, args.warmup)
-        print(json.dumps({"gate_up_us": us, "copy_bytes": COPY_BYTES}))
+        us = layer_kernel_timing(x, logits, weights, args.steps, args.warmup)
+        print(json.dumps({"layer_kernel_us": us, "copy_bytes": COPY_BYTES}))
         return
 
     # A step replays one graph of W_COPIES consecutive layers, one per weight
@@ -426,11 +439,12 @@ def main():
     layer_bytes = hits * (EXPERT_FP8_BYTES + EXPERT_SCALE_BYTES) + M * H * 3 + M * (H // 128) * 4 + M * E * 4
     layer_gbs = layer_bytes / sec / 1e9
 
-    k_us = gate_up_kernel_timing(x, logits, weights, max(args.steps, 50), args.warmup)
-    g1_bytes = hits * (2 * INTER * H + (2 * INTER // 128) * (H // 128) * 4) + M * H * 2 + M * K_TOP * INTER * 2
+    k_us = layer_kernel_timing(x, logits, weights, max(args.steps, 50), args.warmup)
+    g1_bytes = layer_kernel_bytes(M, hits)
     g1_gbs = g1_bytes / (k_us * 1e-6) / 1e9
 
-    traffic = int(GATE_UP_FETCH_KIB * 1024 * FETCH_FACTOR + GATE_UP_WRITE_KIB * 1024 * WRITE_FACTOR)
+    traffic = (int(LAYER_FETCH_KIB * 1024 * FETCH_FACTOR + LAYER_WRITE_KIB * 1024 * WRITE_FACTOR)
+               if LAYER_FETCH_KIB is not None else None)
     out = {
         "metric": "fused FP8 MoE layer us + % HBM/MFMA roofline at M=32 and M=8192",
         "value": round(us, 2),
@@ -450,7 +464,8 @@ def main():
                    "layers_per_step": W_COPIES},
         "layer": {"us": round(us, 2), "single_graph_us": round(single_us, 2), "algorithmic_bytes": layer_bytes, "GBps": round(layer_gbs, 1),
                   "hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
-        "roofline": {"kernel": "stream_fp8_cu_kernel<EPI_ACT> (gate_up + SiLU-and-mul)", "bound": "hbm",
+        "roofline": {"kernel": "stream_fp8_layer_kernel (gate_up + SiLU-and-mul, then down x routed weight)",
+                     "bound": "hbm",
                      "achieved": round(g1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g1_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic if M == 32 else None,

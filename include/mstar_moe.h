@@ -202,6 +202,30 @@ int mstar_moe_stream_gemm(const void* A, int a_dtype, const float* a_scale, cons
                           int64_t num_slots, int num_experts, int64_t N, int64_t K, int top_k,
                           int mul_routed_weight, int activation, void* stream);
 
+/* The routed experts of the FP8 decode layer in ONE launch: the second of
+ * mstar_moe_layer's launches at decode sizes.  The gate_up GEMM (+ SiLU /
+ * GeLU-and-mul) and the down GEMM (x routed weight) of
+ * fused_experts_impl (mstar/utils/fused_moe/runner.py:118-152, the two
+ * invoke_fused_moe_kernel calls) as one weight stream; each workgroup's
+ * down work starts as soon as the gate_up work of its experts is done.
+ *   hq FP8_AS_BF16 [num_tokens, hidden], hs fp32 [num_tokens, hidden/128]
+ *     (as written by mstar_moe_topk_softmax_quant);
+ *   topk_weights fp32, topk_ids int32 [num_tokens * top_k] (valid ids);
+ *   w1 [E, 2*inter, hidden] e4m3fn, w1_scale fp32 [E, 2*inter/128, hidden/128];
+ *   w2 [E, hidden, inter] e4m3fn, w2_scale fp32 [E, hidden/128, inter/128];
+ *   act: bf16 [num_tokens * top_k, inter] scratch (the SiLU-and-mul rows);
+ *   out_rows: bf16 [num_tokens * top_k, hidden], each slot's down row times its
+ *     routed weight (mstar_moe_sum_reduce gives the layer output);
+ *   sync: int32 [num_experts + 1], ZERO when the launch starts (it is not
+ *     cleared again; mstar_moe_layer's routing launch clears its own).
+ * Shapes: hidden 2048, inter 768, num_tokens * top_k <= 1024 (otherwise
+ * MSTAR_UNSUPPORTED). */
+int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, const float* w1_scale,
+                           const void* w2, const float* w2_scale, const float* topk_weights,
+                           const int32_t* topk_ids, int64_t num_tokens, int64_t hidden,
+                           int num_experts, int64_t inter, int top_k, int activation, void* act,
+                           void* out_rows, int32_t* sync, void* stream);
+
 /* Workspace bytes mstar_fused_moe needs for these sizes. */
 int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
                                    int64_t inter, int top_k, int quant, int act_dtype,

@@ -384,6 +384,49 @@ int mstar_moe_stream_gemm(const void* A, int a_dtype, const float* a_scale, cons
   return launch_stream_fp8(g, activation >= 0 ? EPI_ACT : EPI_STORE, true, (hipStream_t)stream);
 }
 
+int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, const float* w1_scale,
+                           const void* w2, const float* w2_scale, const float* topk_weights,
+                           const int32_t* topk_ids, int64_t num_tokens, int64_t hidden,
+                           int num_experts, int64_t inter, int top_k, int activation, void* act,
+                           void* out_rows, int32_t* sync, void* stream) {
+  if (num_tokens < 0 || hidden <= 0 || inter <= 0 || num_experts <= 0 || top_k <= 0 ||
+      top_k > num_experts || activation < 0 || activation > 1) {
+    set_last_error("moe_stream_layer: invalid sizes (M=%lld H=%lld E=%d I=%lld top_k=%d act=%d)",
+                   (long long)num_tokens, (long long)hidden, num_experts, (long long)inter, top_k,
+                   activation);
+    return kInvalidArgument;
+  }
+  const int64_t slots = num_tokens * top_k;
+  if (!stream_fp8_layer_supported(hidden, inter, slots, num_experts)) {
+    set_last_error("moe_stream_layer: unsupported shape (H=%lld I=%lld slots=%lld E=%d)",
+                   (long long)hidden, (long long)inter, (long long)slots, num_experts);
+    return kUnsupported;
+  }
+  if (num_tokens == 0) return kOk;
+  if (!hq || !hs || !w1 || !w1_scale || !w2 || !w2_scale || !topk_weights || !topk_ids || !act ||
+      !out_rows || !sync) {
+    set_last_error("moe_stream_layer: null tensor pointer");
+    return kInvalidArgument;
+  }
+  const int64_t H = hidden, I = inter;
+  GemmArgs g1 = {};
+  g1.A = hq; g1.lda = H; g1.a_scale = hs; g1.ld_as = H / 128; g1.a_q16 = 1;
+  g1.B = w1; g1.ldb = H; g1.b_estride = 2 * I * H; g1.b_scale = w1_scale;
+  g1.bs_ld = H / 128; g1.bs_estride = (2 * I / 128) * (H / 128);
+  g1.C = act; g1.ldc = I;
+  g1.topk_w = topk_weights; g1.topk_w_dtype = kF32;
+  g1.topk_ids = topk_ids; g1.ids_dtype = kI32;
+  g1.M = slots; g1.N = (int)(2 * I); g1.K = (int)H; g1.top_k = top_k; g1.inter = (int)I;
+  g1.activation = activation; g1.num_experts = num_experts;
+  GemmArgs g2 = g1;
+  g2.A = act; g2.lda = I; g2.a_scale = nullptr; g2.ld_as = 0; g2.a_q16 = 0;
+  g2.B = w2; g2.ldb = I; g2.b_estride = H * I; g2.b_scale = w2_scale;
+  g2.bs_ld = I / 128; g2.bs_estride = (H / 128) * (I / 128);
+  g2.C = out_rows; g2.ldc = H;
+  g2.N = (int)H; g2.K = (int)I; g2.top_k = 1; g2.mul_routed = 1;
+  return launch_stream_fp8_layer(g1, g2, sync, (hipStream_t)stream);
+}
+
 int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
                                int num_experts, int block_size, int32_t* sorted_token_ids,
                                int64_t sorted_len, int32_t* expert_ids, int64_t expert_ids_len,

@@ -140,3 +140,65 @@ def test_stream_gemm_rejects_widened_rows_beyond_slot_limit():
                                    _lib.DT_F32, None, _lib.DT_I32, 2048, E, 2 * I, H, K_TOP, 0, 0,
                                    None)
     assert st == 1  # invalid argument: num_slots > 1024
+
+
+def _stream_layer(hq, hs, tw, ti, M, c2, c3, sync=None):
+    from mstar_amd import _lib
+    lib = _lib.load()
+    q1, s1, q2, s2 = _weights()
+    if sync is None:
+        sync = torch.zeros(E + 1, dtype=torch.int32, device=DEV)
+    _lib.check(lib.mstar_moe_stream_layer(
+        hq.data_ptr(), hs.data_ptr(), q1.data_ptr(), s1.data_ptr(), q2.data_ptr(), s2.data_ptr(),
+        tw.data_ptr(), ti.data_ptr(), M, H, E, I, K_TOP, 0, c2.data_ptr(), c3.data_ptr(),
+        sync.data_ptr(), _lib.stream_of(hq)), "moe_stream_layer")
+    return sync
+
+
+@pytest.mark.parametrize("M,skewed", [(32, False), (1, False), (64, False), (128, True)])
+def test_stream_layer_one_launch(M, skewed):
+    """mstar_moe_stream_layer (gate_up and down in one launch, the down work of
+    an expert waiting for its gate_up rows) equals the two-launch composition
+    bit for bit and the oracle within tolerance.  Skewed: every token on the
+    same 8 experts (128 rows each), so both phases stage in windows and every
+    down window waits on gate_up work spread over many workgroups."""
+    from mstar_amd import _lib, ops
+    q1, s1, q2, s2 = _weights()
+    x, logits = _inputs(M, seed=300 + M)
+    tw, ti, hq, hs = _route_quant(x, logits)
+    if skewed:
+        g = torch.Generator().manual_seed(7)
+        ti = torch.stack([torch.randperm(8, generator=g) for _ in range(M)]).int().to(DEV)
+        tw = torch.softmax(torch.randn(M, K_TOP, generator=g), dim=-1).to(DEV)
+    slots = M * K_TOP
+    c2 = torch.empty(slots, I, dtype=torch.bfloat16, device=DEV)
+    c3 = torch.empty(slots, H, dtype=torch.bfloat16, device=DEV)
+    sync = _stream_layer(hq, hs, tw, ti, M, c2, c3)
+    assert int(sync[E]) == 0, "a down-phase wait gave up"
+    c2r = torch.empty_like(c2)
+    c3r = torch.empty_like(c3)
+    _stream_gemm(hq, _lib.DT_FP8_AS_BF16, hs, q1, s1, c2r, tw, ti, slots, 2 * I, H, K_TOP, 0, 0)
+    _stream_gemm(c2r, _lib.DT_BF16, None, q2, s2, c3r, tw, ti, slots, H, I, 1, 1, -1)
+    assert torch.equal(c2, c2r)
+    assert torch.equal(c3, c3r)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    ops.moe_sum_reduce(c3.view(M, K_TOP, H), out, 1.0)
+    ref = _ref(x, tw.cpu(), ti.cpu().long())
+    assert_moe_close(out, ref, what=f"stream layer M={M} skewed={skewed}")
+
+
+def test_stream_layer_repeated_launches_agree():
+    """Twenty launches on fresh sync words give identical rows (the per-expert
+    waits order every read after the matching writes on every launch)."""
+    x, logits = _inputs(32, seed=77)
+    tw, ti, hq, hs = _route_quant(x, logits)
+    slots = 32 * K_TOP
+    c2 = torch.empty(slots, I, dtype=torch.bfloat16, device=DEV)
+    c3 = torch.empty(slots, H, dtype=torch.bfloat16, device=DEV)
+    _stream_layer(hq, hs, tw, ti, 32, c2, c3)
+    first = c3.clone()
+    for _ in range(20):
+        c3.fill_(0)
+        sync = _stream_layer(hq, hs, tw, ti, 32, c2, c3)
+        assert int(sync[E]) == 0
+        assert torch.equal(c3, first)
