@@ -73,8 +73,8 @@ struct Plan {
   // reduced, the down output) are stored by sorted position, so every tile
   // reads and writes contiguous rows; the top-k sum gathers through pos_of.
   bool by_pos = false;
-  // FP8 decode layer: gate_up and down in one streaming launch
-  // (launch_stream_fp8_layer), synchronised per expert through off_sync,
+  // Decode layer (FP8 or W4A16): gate_up and down in one streaming launch
+  // (launch_stream_layer), synchronised per expert through off_sync,
   // which the routing launch clears.
   bool one_launch = false;
   // W4A16 above decode size: the 64-token int4 tile GEMM (gemm_w4.hip).
@@ -145,7 +145,8 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->route_quant = with_route && ((pl->ids_mode && quant == MSTAR_QUANT_FP8_W8A8 && H % 512 == 0) ||
                                    (quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream &&
                                     route_is_grid(M, top_k)));
-  pl->one_launch = pl->route_quant && pl->stream && reduce && stream_fp8_layer_supported(H, I, pl->slots, E);
+  pl->one_launch = with_route && pl->ids_mode && pl->stream && reduce &&
+                   (pl->route_quant || quant == MSTAR_QUANT_W4A16) && stream_layer_supported(H, I, pl->slots, E);
   pl->off_sync = pl->one_launch ? take((size_t)(E + 1) * 4) : 0;
   pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;
   pl->off_hs = fp8_tiled || pl->route_quant ? take((size_t)M * (H / 128) * 4) : 0;
@@ -238,7 +239,7 @@ static int run_experts(const Plan& pl, const void* hidden, int act_dtype, int64_
       g1.a_q16 = 1;
     }
     if (pl.one_launch) {
-      st = launch_stream_fp8_layer(g1, g2, (int*)(ws + pl.off_sync), stream);
+      st = launch_stream_layer(g1, g2, bkind == B_INT4G, (int*)(ws + pl.off_sync), stream);
     } else {
       st = launch_stream_gemm(g1, A_H16, bkind, EPI_ACT, act_dtype, (int)M, stream);
       if (st != kOk) return st;
@@ -397,7 +398,7 @@ int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, cons
     return kInvalidArgument;
   }
   const int64_t slots = num_tokens * top_k;
-  if (!stream_fp8_layer_supported(hidden, inter, slots, num_experts)) {
+  if (!stream_layer_supported(hidden, inter, slots, num_experts)) {
     set_last_error("moe_stream_layer: unsupported shape (H=%lld I=%lld slots=%lld E=%d)",
                    (long long)hidden, (long long)inter, (long long)slots, num_experts);
     return kUnsupported;
@@ -424,7 +425,7 @@ int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, cons
   g2.bs_ld = I / 128; g2.bs_estride = (H / 128) * (I / 128);
   g2.C = out_rows; g2.ldc = H;
   g2.N = (int)H; g2.K = (int)I; g2.top_k = 1; g2.mul_routed = 1;
-  return launch_stream_fp8_layer(g1, g2, sync, (hipStream_t)stream);
+  return launch_stream_layer(g1, g2, false, sync, (hipStream_t)stream);
 }
 
 int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,

@@ -172,12 +172,12 @@ constexpr int kBigBlockM = 256;
 // otherwise with the FP8 MFMA.
 int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream);
 constexpr int64_t kStreamMaxIdsSlots = 1024;  // slots a launch in ids mode can take
-// The FP8 decode layer's gate_up and down streaming GEMMs in one launch
-// (g1: gate_up on the routing launch's widened FP8 token rows; g2: down on
-// g1's bf16 output).  sync_words: E + 1 ints, zero when the launch starts
-// (the routing launch clears them).
-bool stream_fp8_layer_supported(int64_t H, int64_t I, int64_t slots, int E);
-int launch_stream_fp8_layer(const GemmArgs& g1, const GemmArgs& g2, int* sync_words, hipStream_t stream);
+// The decode layer's gate_up and down streaming GEMMs in one launch (g1:
+// gate_up on the routing launch's widened FP8 token rows, or int4 on bf16
+// hidden rows; g2: down on g1's bf16 output).  sync_words: E + 1 ints, zero
+// when the launch starts (the routing launch clears them).
+bool stream_layer_supported(int64_t H, int64_t I, int64_t slots, int E);
+int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* sync_words, hipStream_t stream);
 bool stream_fp8_supported(int K, int N, int inter, int epi);
 
 

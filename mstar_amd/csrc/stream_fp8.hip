@@ -458,7 +458,7 @@ __device__ uint64_t g_timeline[2 * 1024 * 8];  // [EPI][workgroup][phase]
   } while (0)
 #endif
 
-// The decode layer in one launch (stream_fp8_layer_kernel): the gate_up
+// The decode layer in one launch (stream_layer_kernel): the gate_up
 // phase of a workgroup reports, per expert, the (item, token row) pairs it
 // finished; the down phase stages an expert's activation rows only once
 // all of that expert's gate_up pairs are reported.
@@ -475,8 +475,8 @@ constexpr uint64_t kLayerWaitTicks = 2000000;
 // One workgroup's share of a streaming GEMM: work range `wg` of `nwg`.
 template <int EPI, int KS, int STAGE, int PHASE = kPhaseAlone>
 __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int wg, int nwg, const LayerSync& ls) {
-  static_assert(PHASE == kPhaseAlone || (STAGE != STAGE_W4 && (PHASE == kPhaseGate) == (EPI == EPI_ACT)),
-                "layer phases: FP8 gate_up, then FP8 down");
+  static_assert(PHASE == kPhaseAlone || (PHASE == kPhaseGate) == (EPI == EPI_ACT),
+                "layer phases: gate_up, then down");
   constexpr bool W4 = STAGE == STAGE_W4;
   static_assert(!W4 || KS % 2 == 0, "int4 chunks are two K-steps");
   constexpr int PITCH = cu_pitch<KS>();
@@ -753,7 +753,7 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
         const int gq = g0 + j * (ST / 16) + (tid >> 4), sub = tid & 15;
         const bool live = gq < groups;
         const int r = live ? gq / KS : 0, ks = live ? gq - (gq / KS) * KS : 0;
-        raw[j] = live ? *(const v4i*)(A16 + (int64_t)arow_of(r) * p.lda + ks * 128 + sub * 8)
+        raw[j] = live ? load_rows16<PHASE == kPhaseDown>(A16 + (int64_t)arow_of(r) * p.lda + ks * 128 + sub * 8)
                       : v4i{0, 0, 0, 0};
       }
 #pragma unroll
@@ -1099,20 +1099,21 @@ __device__ __forceinline__ int xcd_range(int b, int nwg) {
   return nwg % 8 == 0 ? (b % 8) * (nwg / 8) + b / 8 : b;
 }
 
-// The FP8 decode layer's two streaming GEMMs in one launch: each workgroup
-// runs its gate_up range (bf16-widened FP8 token rows from the routing
-// launch -> bf16 SiLU-and-mul rows), then its down range, staging an
-// expert's rows once the gate_up phases that cover the expert reported
-// them (LayerSync).  Every workgroup's gate_up phase runs without waiting,
-// so the waits end as long as the workgroups a wait depends on are
-// resident; a wait that passes kLayerWaitTicks sets ls.err and goes on.
-template <int KS1, int KS2>
-__global__ __launch_bounds__(kCuThreads) void stream_fp8_layer_kernel(GemmArgs g1, GemmArgs g2, int cap1, int cap2,
-                                                                      LayerSync ls) {
+// The decode layer's two streaming GEMMs in one launch: each workgroup
+// runs its gate_up range (FP8: bf16-widened FP8 token rows from the routing
+// launch; W4: bf16 hidden rows -> bf16 SiLU-and-mul rows), then its down
+// range, staging an expert's rows once the gate_up phases that cover the
+// expert reported them (LayerSync).  Every workgroup's gate_up phase runs
+// without waiting, so the waits end as long as the workgroups a wait depends
+// on are resident; a wait that passes kLayerWaitTicks sets ls.err and goes on.
+template <int KS1, int KS2, bool W4>
+__global__ __launch_bounds__(W4 ? kCuThreadsW4 : kCuThreads) void stream_layer_kernel(GemmArgs g1, GemmArgs g2,
+                                                                                   int cap1, int cap2,
+                                                                                   LayerSync ls) {
   const int r = xcd_range(blockIdx.x, gridDim.x);
-  stream_cu_body<EPI_ACT, KS1, STAGE_Q16, kPhaseGate>(g1, cap1, r, gridDim.x, ls);
+  stream_cu_body<EPI_ACT, KS1, W4 ? STAGE_W4 : STAGE_Q16, kPhaseGate>(g1, cap1, r, gridDim.x, ls);
   __syncthreads();  // every wave is done with the gate_up phase's LDS
-  stream_cu_body<EPI_STORE, KS2, STAGE_H16, kPhaseDown>(g2, cap2, r, gridDim.x, ls);
+  stream_cu_body<EPI_STORE, KS2, W4 ? STAGE_W4 : STAGE_H16, kPhaseDown>(g2, cap2, r, gridDim.x, ls);
 }
 
 
@@ -1176,51 +1177,51 @@ static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, in
   return true;
 }
 
-// Rows a window of the CU-resident FP8 kernel stages, and its dynamic LDS.
-template <int KS>
+// Rows a window of the CU-resident kernel stages, and its dynamic LDS.
+template <int KS, bool W4>
 static bool cu_window(const GemmArgs& a, int* cap_out, size_t* shmem_out) {
   const size_t per_row = (size_t)cu_pitch<KS>() + (KS + 1) * 4;
-  const size_t fixed = cu_sc_off<KS>(a.num_experts, a.M) + 16 + 1024;
+  const size_t fixed = cu_sc_off<KS, W4>(a.num_experts, a.M) + 16 + 1024;
   if (fixed + 4 * per_row > kCuLdsMax) return false;
   int cap = (int)((kCuLdsMax - fixed) / per_row);
   if (cap > 1024) cap = 1024;
   *cap_out = cap;
-  *shmem_out = cu_rows_off<KS>(a.num_experts, a.M, cap) + (size_t)cap * cu_pitch<KS>();
+  *shmem_out = cu_rows_off<KS, W4>(a.num_experts, a.M, cap) + (size_t)cap * cu_pitch<KS>();
   return true;
 }
 
-template <int KS1, int KS2>
-static int run_stream_fp8_layer(const GemmArgs& g1, const GemmArgs& g2, const LayerSync& ls,
-                                hipStream_t stream) {
+template <int KS1, int KS2, bool W4>
+static int run_stream_layer(const GemmArgs& g1, const GemmArgs& g2, const LayerSync& ls, hipStream_t stream) {
   int cap1, cap2;
   size_t sh1, sh2;
-  if (!cu_window<KS1>(g1, &cap1, &sh1) || !cu_window<KS2>(g2, &cap2, &sh2)) {
-    set_last_error("stream_fp8_layer: the windows do not fit in LDS");
+  if (!cu_window<KS1, W4>(g1, &cap1, &sh1) || !cu_window<KS2, W4>(g2, &cap2, &sh2)) {
+    set_last_error("stream_layer: the windows do not fit in LDS");
     return kUnsupported;
   }
   const size_t shmem = sh1 > sh2 ? sh1 : sh2;
-  auto kern = stream_fp8_layer_kernel<KS1, KS2>;
-  const int st = ensure_dynamic_lds((const void*)kern, shmem, "stream_fp8_layer");
+  auto kern = stream_layer_kernel<KS1, KS2, W4>;
+  const int st = ensure_dynamic_lds((const void*)kern, shmem, "stream_layer");
   if (st != kOk) return st;
-  kern<<<dim3(device_cu_count()), dim3(kCuThreads), shmem, stream>>>(g1, g2, cap1, cap2, ls);
-  return launch_status("stream_fp8_layer");
+  kern<<<dim3(device_cu_count()), dim3(W4 ? kCuThreadsW4 : kCuThreads), shmem, stream>>>(g1, g2, cap1, cap2, ls);
+  return launch_status("stream_layer");
 }
 
-bool stream_fp8_layer_supported(int64_t H, int64_t I, int64_t slots, int E) {
+bool stream_layer_supported(int64_t H, int64_t I, int64_t slots, int E) {
   return H == 2048 && I == 768 && slots <= kStreamMaxIdsSlots && E <= 1024;
 }
 
-int launch_stream_fp8_layer(const GemmArgs& g1, const GemmArgs& g2, int* sync_words, hipStream_t stream) {
-  if (!stream_fp8_layer_supported(g1.K, g1.inter, g1.M, g1.num_experts) || !g1.topk_ids || !g2.topk_ids ||
-      !g1.a_q16 || !g1.a_scale || g2.a_scale || g2.K != g1.inter || g2.N != g1.K || !sync_words) {
-    set_last_error("stream_fp8_layer: unsupported configuration");
+int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* sync_words, hipStream_t stream) {
+  const bool rows_ok = int4 ? (!g1.a_q16 && !g1.a_scale) : (g1.a_q16 && g1.a_scale);
+  if (!stream_layer_supported(g1.K, g1.inter, g1.M, g1.num_experts) || !g1.topk_ids || !g2.topk_ids ||
+      !rows_ok || g2.a_scale || g2.K != g1.inter || g2.N != g1.K || !sync_words) {
+    set_last_error("stream_layer: unsupported configuration");
     return kUnsupported;
   }
   LayerSync ls;
   ls.done = sync_words;
   ls.err = sync_words + g1.num_experts;
   ls.gate_ipe = g1.inter / 8;
-  return run_stream_fp8_layer<16, 6>(g1, g2, ls, stream);
+  return int4 ? run_stream_layer<16, 6, true>(g1, g2, ls, stream) : run_stream_layer<16, 6, false>(g1, g2, ls, stream);
 }
 
 int launch_stream_int4_cu(const GemmArgs& a, int epi, hipStream_t stream) {
