@@ -208,14 +208,15 @@ def layer_kernel_timing(x, logits, weights, steps, warmup):
 
     for i in range(warmup):
         launch(i, weights[i % len(weights)])
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # An event pair around every launch: host gaps between launches stay out.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
-    start.record(stream)
     for i in range(steps):
+        ev[i][0].record(stream)
         launch(warmup + i, weights[i % len(weights)])
-    end.record(stream)
-    end.synchronize()
-    return start.elapsed_time(end) * 1e3 / steps  # us
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) * 1e3 / steps  # us
 
 
 def dense_fp8_lines(args, K=2048):
