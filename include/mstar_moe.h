@@ -218,7 +218,7 @@ int mstar_moe_stream_gemm(const void* A, int a_dtype, const float* a_scale, cons
  *     routed weight (mstar_moe_sum_reduce gives the layer output);
  *   sync: int32 [num_experts + 1], ZERO when the launch starts (it is not
  *     cleared again; mstar_moe_layer's routing launch clears its own).
- * Shapes: hidden 2048, inter 768, num_tokens * top_k <= 1024 (otherwise
+ * Shapes: (hidden, inter) = (2048, 768) or (1024, 384), num_tokens * top_k <= 1024 (otherwise
  * MSTAR_UNSUPPORTED). */
 int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, const float* w1_scale,
                            const void* w2, const float* w2_scale, const float* topk_weights,

@@ -146,7 +146,8 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
                                    (quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream &&
                                     route_is_grid(M, top_k)));
   pl->one_launch = with_route && pl->ids_mode && pl->stream && reduce &&
-                   (pl->route_quant || quant == MSTAR_QUANT_W4A16) && stream_layer_supported(H, I, pl->slots, E);
+                   (pl->route_quant || quant == MSTAR_QUANT_W4A16) &&
+                   stream_layer_supported(H, I, pl->slots, E, quant == MSTAR_QUANT_W4A16);
   pl->off_sync = pl->one_launch ? take((size_t)(E + 1) * 4) : 0;
   pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;
   pl->off_hs = fp8_tiled || pl->route_quant ? take((size_t)M * (H / 128) * 4) : 0;
@@ -398,7 +399,7 @@ int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, cons
     return kInvalidArgument;
   }
   const int64_t slots = num_tokens * top_k;
-  if (!stream_layer_supported(hidden, inter, slots, num_experts)) {
+  if (!stream_layer_supported(hidden, inter, slots, num_experts, false)) {
     set_last_error("moe_stream_layer: unsupported shape (H=%lld I=%lld slots=%lld E=%d)",
                    (long long)hidden, (long long)inter, (long long)slots, num_experts);
     return kUnsupported;

@@ -176,7 +176,7 @@ constexpr int64_t kStreamMaxIdsSlots = 1024;  // slots a launch in ids mode can 
 // gate_up on the routing launch's widened FP8 token rows, or int4 on bf16
 // hidden rows; g2: down on g1's bf16 output).  sync_words: E + 1 ints, zero
 // when the launch starts (the routing launch clears them).
-bool stream_layer_supported(int64_t H, int64_t I, int64_t slots, int E);
+bool stream_layer_supported(int64_t H, int64_t I, int64_t slots, int E, bool int4);
 int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* sync_words, hipStream_t stream);
 bool stream_fp8_supported(int K, int N, int inter, int epi);
 

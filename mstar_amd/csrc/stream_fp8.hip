@@ -402,12 +402,12 @@ __host__ __device__ inline size_t cu_lists_bytes(int E, int64_t M) {
   return ((size_t)3 * E + (size_t)((M + 3) & ~3ll) + 32) * 4;
 }
 template <int KS, bool W4 = false>
-__host__ __device__ inline size_t cu_sc_off(int E, int64_t M) {
-  return cu_ring_bytes<KS, W4>() + cu_lists_bytes(E, M);
+__host__ __device__ inline size_t cu_sc_off(int E, int64_t M, size_t lists_at = 0) {
+  return (lists_at ? lists_at : cu_ring_bytes<KS, W4>()) + cu_lists_bytes(E, M);
 }
 template <int KS, bool W4 = false>
-__host__ __device__ inline size_t cu_rows_off(int E, int64_t M, int cap) {
-  return (cu_sc_off<KS, W4>(E, M) + (size_t)cap * (KS + 1) * 4 + 15) & ~(size_t)15;
+__host__ __device__ inline size_t cu_rows_off(int E, int64_t M, int cap, size_t lists_at = 0) {
+  return (cu_sc_off<KS, W4>(E, M, lists_at) + (size_t)cap * (KS + 1) * 4 + 15) & ~(size_t)15;
 }
 
 // Wait for the oldest of `ahead` chunks in flight (DPC DMA instructions
@@ -467,6 +467,7 @@ struct LayerSync {
   int* done;       // [E] gate_up (item, token row) pairs finished per expert; zero at launch
   int* err;        // set to 1 if a wait gave up (output of that launch invalid)
   int gate_ipe;    // gate_up items per expert (inter / 8)
+  int lists_at;    // LDS offset of the expert lists (after both phases' rings)
 };
 // Longest wait of the down phase for an expert's gate_up rows before it
 // gives up (s_memrealtime ticks of 10 ns): 20 ms.
@@ -499,13 +500,15 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
   typedef __attribute__((address_space(3))) void* lds_void_ptr;
   extern __shared__ __align__(16) uint8_t smem[];
   const int E = p.num_experts;
-  int* sAct = (int*)(smem + cu_ring_bytes<KS, W4>());
+  // The layer kernel puts the lists after the larger of its two phases' rings.
+  const size_t lists_at = PHASE == kPhaseAlone ? 0 : (size_t)ls.lists_at;
+  int* sAct = (int*)(smem + (lists_at ? lists_at : cu_ring_bytes<KS, W4>()));
   int* sCnt = sAct + E;
   int* sOff = sCnt + E;
   int* sList = sOff + E;
-  float* sSc = (float*)(smem + cu_sc_off<KS, W4>(E, p.M));
+  float* sSc = (float*)(smem + cu_sc_off<KS, W4>(E, p.M, lists_at));
   float* sRw = sSc + cap * KS;  // routed weight of each staged row
-  uint8_t* sRows = smem + cu_rows_off<KS, W4>(E, p.M, cap);
+  uint8_t* sRows = smem + cu_rows_off<KS, W4>(E, p.M, cap, lists_at);
   uint32_t* sMask = (uint32_t*)(sList + ((p.M + 3) & ~3ll));  // [32] active experts (E <= 1024)
   // The down phase of the layer kernel finds the lists the gate_up phase
   // built from the same router ids.
@@ -1179,22 +1182,24 @@ static bool try_stream_fp8_cu(const GemmArgs& a, int epi, hipStream_t stream, in
 
 // Rows a window of the CU-resident kernel stages, and its dynamic LDS.
 template <int KS, bool W4>
-static bool cu_window(const GemmArgs& a, int* cap_out, size_t* shmem_out) {
+static bool cu_window(const GemmArgs& a, size_t lists_at, int* cap_out, size_t* shmem_out) {
   const size_t per_row = (size_t)cu_pitch<KS>() + (KS + 1) * 4;
-  const size_t fixed = cu_sc_off<KS, W4>(a.num_experts, a.M) + 16 + 1024;
+  const size_t fixed = cu_sc_off<KS, W4>(a.num_experts, a.M, lists_at) + 16 + 1024;
   if (fixed + 4 * per_row > kCuLdsMax) return false;
   int cap = (int)((kCuLdsMax - fixed) / per_row);
   if (cap > 1024) cap = 1024;
   *cap_out = cap;
-  *shmem_out = cu_rows_off<KS, W4>(a.num_experts, a.M, cap) + (size_t)cap * cu_pitch<KS>();
+  *shmem_out = cu_rows_off<KS, W4>(a.num_experts, a.M, cap, lists_at) + (size_t)cap * cu_pitch<KS>();
   return true;
 }
 
 template <int KS1, int KS2, bool W4>
-static int run_stream_layer(const GemmArgs& g1, const GemmArgs& g2, const LayerSync& ls, hipStream_t stream) {
+static int run_stream_layer(const GemmArgs& g1, const GemmArgs& g2, LayerSync ls, hipStream_t stream) {
   int cap1, cap2;
   size_t sh1, sh2;
-  if (!cu_window<KS1, W4>(g1, &cap1, &sh1) || !cu_window<KS2, W4>(g2, &cap2, &sh2)) {
+  const size_t r1 = cu_ring_bytes<KS1, W4>(), r2 = cu_ring_bytes<KS2, W4>();
+  ls.lists_at = (int)(r1 > r2 ? r1 : r2);
+  if (!cu_window<KS1, W4>(g1, ls.lists_at, &cap1, &sh1) || !cu_window<KS2, W4>(g2, ls.lists_at, &cap2, &sh2)) {
     set_last_error("stream_layer: the windows do not fit in LDS");
     return kUnsupported;
   }
@@ -1206,13 +1211,16 @@ static int run_stream_layer(const GemmArgs& g1, const GemmArgs& g2, const LayerS
   return launch_status("stream_layer");
 }
 
-bool stream_layer_supported(int64_t H, int64_t I, int64_t slots, int E) {
-  return H == 2048 && I == 768 && slots <= kStreamMaxIdsSlots && E <= 1024;
+// (H, I): the Qwen3-Omni thinker (2048, 768) and talker (1024, 384) MoE
+// shapes; int4 weights need I % 256 == 0.
+bool stream_layer_supported(int64_t H, int64_t I, int64_t slots, int E, bool int4) {
+  const bool shape = (H == 2048 && I == 768) || (!int4 && H == 1024 && I == 384);
+  return shape && slots <= kStreamMaxIdsSlots && E <= 1024;
 }
 
 int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* sync_words, hipStream_t stream) {
   const bool rows_ok = int4 ? (!g1.a_q16 && !g1.a_scale) : (g1.a_q16 && g1.a_scale);
-  if (!stream_layer_supported(g1.K, g1.inter, g1.M, g1.num_experts) || !g1.topk_ids || !g2.topk_ids ||
+  if (!stream_layer_supported(g1.K, g1.inter, g1.M, g1.num_experts, int4) || !g1.topk_ids || !g2.topk_ids ||
       !rows_ok || g2.a_scale || g2.K != g1.inter || g2.N != g1.K || !sync_words) {
     set_last_error("stream_layer: unsupported configuration");
     return kUnsupported;
@@ -1221,7 +1229,9 @@ int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* 
   ls.done = sync_words;
   ls.err = sync_words + g1.num_experts;
   ls.gate_ipe = g1.inter / 8;
-  return int4 ? run_stream_layer<16, 6, true>(g1, g2, ls, stream) : run_stream_layer<16, 6, false>(g1, g2, ls, stream);
+  if (int4) return run_stream_layer<16, 6, true>(g1, g2, ls, stream);
+  return g1.K == 2048 ? run_stream_layer<16, 6, false>(g1, g2, ls, stream)
+                      : run_stream_layer<8, 3, false>(g1, g2, ls, stream);
 }
 
 int launch_stream_int4_cu(const GemmArgs& a, int epi, hipStream_t stream) {

@@ -202,3 +202,48 @@ def test_stream_layer_repeated_launches_agree():
         sync = _stream_layer(hq, hs, tw, ti, 32, c2, c3)
         assert int(sync[E]) == 0
         assert torch.equal(c3, first)
+
+
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_moe_layer_one_launch_talker_shape(M):
+    """The Qwen3-Omni talker MoE shape (hidden 1024, inter 384, 128 experts,
+    top-8) through mstar_moe_layer, whose decode sizes run the experts in one
+    launch (its lists sit after the larger of the two phases' rings, the
+    3-step down ring): equal to the two-launch composition bit for bit and to
+    the oracle within tolerance."""
+    from mstar_amd import _lib, ops, quant
+    Ht, It = 1024, 384
+    g = torch.Generator().manual_seed(21)
+    w1 = (torch.randn(E, 2 * It, Ht, generator=g) * 0.02).to(DEV)
+    w2 = (torch.randn(E, Ht, It, generator=g) * 0.02).to(DEV)
+    q1, s1 = quant.quantize_fp8_block(w1)
+    q2, s2 = quant.quantize_fp8_block(w2)
+    x = torch.randn(M, Ht, generator=g).to(torch.bfloat16)
+    logits = torch.randn(M, E, generator=g)
+    out, tw, ti = ops.moe_layer(x.to(DEV), logits.to(DEV), q1, q2, K_TOP, True, 0, _lib.QUANT_FP8_W8A8, s1, s2)
+    lib = _lib.load()
+    tw2 = torch.empty(M, K_TOP, dtype=torch.float32, device=DEV)
+    ti2 = torch.empty(M, K_TOP, dtype=torch.int32, device=DEV)
+    hq = torch.empty(M, Ht, dtype=torch.bfloat16, device=DEV)
+    hs = torch.empty(M, Ht // 128, dtype=torch.float32, device=DEV)
+    xd, ld = x.to(DEV), logits.to(DEV)
+    _lib.check(lib.mstar_moe_topk_softmax_quant(
+        ld.data_ptr(), _lib.DT_F32, M, E, K_TOP, 1, tw2.data_ptr(), ti2.data_ptr(), None,
+        xd.data_ptr(), Ht, hq.data_ptr(), hs.data_ptr(), _lib.stream_of(xd)), "topk_softmax_quant")
+    slots = M * K_TOP
+    c2 = torch.empty(slots, It, dtype=torch.bfloat16, device=DEV)
+    c3 = torch.empty(slots, Ht, dtype=torch.bfloat16, device=DEV)
+    for A, a_dt, a_s, B, b_s, C, N, Kd, tk, mul, act in (
+            (hq, _lib.DT_FP8_AS_BF16, hs, q1, s1, c2, 2 * It, Ht, K_TOP, 0, 0),
+            (c2, _lib.DT_BF16, None, q2, s2, c3, Ht, It, 1, 1, -1)):
+        _lib.check(lib.mstar_moe_stream_gemm(
+            A.data_ptr(), a_dt, _lib.ptr(a_s), B.data_ptr(), b_s.data_ptr(), C.data_ptr(),
+            tw2.data_ptr(), _lib.DT_F32, ti2.data_ptr(), _lib.DT_I32, slots, E, N, Kd,
+            tk, mul, act, _lib.stream_of(A)), "moe_stream_gemm")
+    ref2 = torch.empty(M, Ht, dtype=torch.bfloat16, device=DEV)
+    ops.moe_sum_reduce(c3.view(M, K_TOP, Ht), ref2, 1.0)
+    assert torch.equal(out, ref2)
+    rw, rids = O.router_topk_softmax(logits, K_TOP, True)
+    ref = O.fused_experts_rounding(x, None, None, rw, rids, w1_dq=O.dequant_fp8_block(q1.cpu(), s1.cpu()),
+                                   w2_dq=O.dequant_fp8_block(q2.cpu(), s2.cpu()), act_quant=True)
+    assert_moe_close(out, ref, what=f"moe_layer talker M={M}")
