@@ -226,6 +226,16 @@ int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, cons
                            int num_experts, int64_t inter, int top_k, int activation, void* act,
                            void* out_rows, int32_t* sync, void* stream);
 
+/* Number of waits of the one-launch decode layer kernel (mstar_moe_layer at
+ * decode sizes, mstar_moe_stream_layer) that gave up on the current device
+ * since the library was loaded; a launch with such a wait produced invalid
+ * output.  The kernel's workgroups wait on each other, which needs them all
+ * resident: never the case while another such launch runs on the device.
+ * Setting MSTAR_MOE_ONE_LAUNCH=0 in the environment makes mstar_moe_layer
+ * use the two-launch form, which has no such wait.  No counterpart in the
+ * reference (a diagnostic of this library's kernel). */
+int mstar_moe_layer_wait_failures(int* count);
+
 /* Workspace bytes mstar_fused_moe needs for these sizes. */
 int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,
                                    int64_t inter, int top_k, int quant, int act_dtype,

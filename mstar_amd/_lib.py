@@ -65,6 +65,7 @@ SIGNATURES = {
     "mstar_moe_stream_layer": (
         _c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_i64, _c_int,
                  _c_int, _vp, _vp, _vp, _vp]),
+    "mstar_moe_layer_wait_failures": (_c_int, [ctypes.POINTER(_c_int)]),
     "mstar_fused_moe_workspace_size": (
         _c_int, [_c_i64, _c_i64, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int,
                  ctypes.POINTER(ctypes.c_size_t)]),

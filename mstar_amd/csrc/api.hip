@@ -10,6 +10,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <stdlib.h>
+
 #include "common.h"
 #include "launch.h"
 #include "../../include/mstar_moe.h"
@@ -87,6 +89,19 @@ struct Plan {
       off_cq, off_cs, off_scratch, scratch_bytes, off_tw, off_ids, off_pos, off_w4h, off_w4hx, off_w4cx, off_sync, total;
 };
 
+// The one-launch decode layer kernel, unless MSTAR_MOE_ONE_LAUNCH=0 in the
+// environment (read once): its workgroups wait on each other, so two such
+// launches must not share a device at the same time; callers that run
+// decode layers concurrently on several streams of one device turn it off
+// and get the two-launch form, which has no such wait.
+static bool one_launch_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("MSTAR_MOE_ONE_LAUNCH");
+    return !(v && v[0] == '0' && v[1] == 0);
+  }();
+  return on;
+}
+
 // with_route: the plan also holds the router outputs and the routing scratch
 // (mstar_moe_layer); otherwise only the alignment scratch (mstar_fused_moe).
 static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quant, int act_dtype,
@@ -145,7 +160,7 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->route_quant = with_route && ((pl->ids_mode && quant == MSTAR_QUANT_FP8_W8A8 && H % 512 == 0) ||
                                    (quant == MSTAR_QUANT_FP8_W8A8 && !pl->stream &&
                                     route_is_grid(M, top_k)));
-  pl->one_launch = with_route && pl->ids_mode && pl->stream && reduce &&
+  pl->one_launch = one_launch_enabled() && with_route && pl->ids_mode && pl->stream && reduce &&
                    (pl->route_quant || quant == MSTAR_QUANT_W4A16) &&
                    stream_layer_supported(H, I, pl->slots, E, quant == MSTAR_QUANT_W4A16);
   pl->off_sync = pl->one_launch ? take((size_t)(E + 1) * 4) : 0;
@@ -428,6 +443,8 @@ int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, cons
   g2.N = (int)H; g2.K = (int)I; g2.top_k = 1; g2.mul_routed = 1;
   return launch_stream_layer(g1, g2, false, sync, (hipStream_t)stream);
 }
+
+int mstar_moe_layer_wait_failures(int* count) { return layer_wait_failures(count); }
 
 int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
                                int num_experts, int block_size, int32_t* sorted_token_ids,

@@ -178,6 +178,8 @@ constexpr int64_t kStreamMaxIdsSlots = 1024;  // slots a launch in ids mode can 
 // when the launch starts (the routing launch clears them).
 bool stream_layer_supported(int64_t H, int64_t I, int64_t slots, int E, bool int4);
 int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* sync_words, hipStream_t stream);
+// Waits of the layer kernel that gave up on the current device (synchronous copy).
+int layer_wait_failures(int* count);
 bool stream_fp8_supported(int K, int N, int inter, int epi);
 
 

@@ -469,6 +469,9 @@ struct LayerSync {
   int gate_ipe;    // gate_up items per expert (inter / 8)
   int lists_at;    // LDS offset of the expert lists (after both phases' rings)
 };
+// Waits of the layer kernel that gave up (kLayerWaitTicks), on this device,
+// since the library was loaded: read by mstar_moe_layer_wait_failures.
+__device__ int g_layer_wait_failures;
 // Longest wait of the down phase for an expert's gate_up rows before it
 // gives up (s_memrealtime ticks of 10 ns): 20 ms.
 constexpr uint64_t kLayerWaitTicks = 2000000;
@@ -1047,6 +1050,7 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
           while (__hip_atomic_load(ls.done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
             if (__builtin_amdgcn_s_memrealtime() - t0 > kLayerWaitTicks) {
               __hip_atomic_store(ls.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_fetch_add(&g_layer_wait_failures, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
               break;
             }
             __builtin_amdgcn_s_sleep(32);
@@ -1232,6 +1236,19 @@ int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* 
   if (int4) return run_stream_layer<16, 6, true>(g1, g2, ls, stream);
   return g1.K == 2048 ? run_stream_layer<16, 6, false>(g1, g2, ls, stream)
                       : run_stream_layer<8, 3, false>(g1, g2, ls, stream);
+}
+
+int layer_wait_failures(int* count) {
+  if (!count) {
+    set_last_error("moe_layer_wait_failures: null pointer");
+    return kInvalidArgument;
+  }
+  if (hipMemcpyFromSymbol(count, HIP_SYMBOL(g_layer_wait_failures), sizeof(int), 0, hipMemcpyDeviceToHost) !=
+      hipSuccess) {
+    set_last_error("moe_layer_wait_failures: reading the counter failed");
+    return kLaunchError;
+  }
+  return kOk;
 }
 
 int launch_stream_int4_cu(const GemmArgs& a, int epi, hipStream_t stream) {

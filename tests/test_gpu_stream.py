@@ -247,3 +247,53 @@ def test_moe_layer_one_launch_talker_shape(M):
     ref = O.fused_experts_rounding(x, None, None, rw, rids, w1_dq=O.dequant_fp8_block(q1.cpu(), s1.cpu()),
                                    w2_dq=O.dequant_fp8_block(q2.cpu(), s2.cpu()), act_quant=True)
     assert_moe_close(out, ref, what=f"moe_layer talker M={M}")
+
+
+def test_layer_wait_failures_stay_zero():
+    """No wait of the one-launch layer kernel gave up in this process (every
+    launch above had its workgroups resident together)."""
+    import ctypes
+    from mstar_amd import _lib
+    lib = _lib.load()
+    x, logits = _inputs(32, seed=78)
+    tw, ti, hq, hs = _route_quant(x, logits)
+    c2 = torch.empty(256, I, dtype=torch.bfloat16, device=DEV)
+    c3 = torch.empty(256, H, dtype=torch.bfloat16, device=DEV)
+    _stream_layer(hq, hs, tw, ti, 32, c2, c3)
+    torch.cuda.synchronize()
+    n = ctypes.c_int(-1)
+    _lib.check(lib.mstar_moe_layer_wait_failures(ctypes.byref(n)), "moe_layer_wait_failures")
+    assert n.value == 0
+
+
+_OPT_OUT_CHILD = r'''
+import sys, torch
+from mstar_amd import _lib, ops, quant
+d = torch.load(sys.argv[1], weights_only=True)
+q1, s1, q2, s2 = (d[k].cuda() for k in ("q1", "s1", "q2", "s2"))
+out = ops.moe_layer(d["x"].cuda(), d["logits"].cuda(), q1, q2, 8, True, 0, _lib.QUANT_FP8_W8A8, s1, s2)[0]
+torch.save({"out": out.cpu()}, sys.argv[2])
+'''
+
+
+def test_one_launch_opt_out_gives_the_same_layer(tmp_path):
+    """MSTAR_MOE_ONE_LAUNCH=0 (for callers that run decode layers on several
+    streams of one device at once) switches mstar_moe_layer to the two-launch
+    form; its output equals the one-launch layer bit for bit."""
+    import os
+    import subprocess
+    import sys
+    from mstar_amd import _lib, ops
+    q1, s1, q2, s2 = _weights()
+    x, logits = _inputs(32, seed=79)
+    out = ops.moe_layer(x.to(DEV), logits.to(DEV), q1, q2, K_TOP, True, 0, _lib.QUANT_FP8_W8A8, s1, s2)[0]
+    torch.save({"x": x, "logits": logits, "q1": q1.cpu(), "s1": s1.cpu(), "q2": q2.cpu(), "s2": s2.cpu()},
+               tmp_path / "in.pt")
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, MSTAR_MOE_ONE_LAUNCH="0", PYTHONPATH=repo + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    print("child: moe_layer with MSTAR_MOE_ONE_LAUNCH=0", flush=True)
+    r = subprocess.run([sys.executable, "-c", _OPT_OUT_CHILD, str(tmp_path / "in.pt"), str(tmp_path / "out.pt")],
+                       cwd=repo, env=env, capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0, r.stderr[-3000:]
+    other = torch.load(tmp_path / "out.pt", weights_only=True)["out"]
+    assert torch.equal(out.cpu(), other)
