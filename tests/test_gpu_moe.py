@@ -490,3 +490,49 @@ def test_fused_experts_fp8_big_tile_path(M, E, k, H, I, bias):
     out = fused_experts(x.to(DEV), q1, q2, tw.to(DEV), ti.to(DEV), quant="fp8_w8a8",
                         w1_scale=s1, w2_scale=s2)
     assert_moe_close(out, _fp8_ref(x, q1, s1, q2, s2, tw, ti), what=f"fp8 big tile M={M}")
+
+
+@pytest.mark.parametrize("quant", ["fp8_w8a8", "w4a16"])
+def test_one_launch_layer_under_hip_graph_replays(quant):
+    """mstar_moe_layer at decode size (routing launch, then the experts in one
+    launch whose per-expert counters the routing launch clears) captured three
+    layers to a graph: every replay equals the eager result bit for bit, with
+    eager layers in between, and no wait of the layer kernel gave up."""
+    import ctypes
+    from mstar_amd import _lib, ops, quant as Q
+    H, E, I, k, M = 2048, 128, 768, 8, 32
+    if quant == "fp8_w8a8":
+        q1, s1, q2, s2 = _fp8_weights(H, E, I)
+        qc = _lib.QUANT_FP8_W8A8
+    else:
+        g = torch.Generator().manual_seed(5)
+        w1 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(DEV)
+        w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(DEV)
+        q1, s1 = Q.quantize_int4_group(w1)
+        q2, s2 = Q.quantize_int4_group(w2)
+        qc = _lib.QUANT_W4A16
+    xs = [_hidden(M, H, seed=40 + i).to(DEV) for i in range(3)]
+    ls = [torch.randn(M, E, device=DEV) for _ in range(3)]
+
+    def fn():
+        return [ops.moe_layer(x, l, q1, q2, k, True, 0, qc, s1, s2)[0] for x, l in zip(xs, ls)]
+
+    eager = [o.clone() for o in fn()]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = fn()
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e)
+        _ = fn()
+        torch.cuda.synchronize()
+    n = ctypes.c_int(-1)
+    _lib.check(_lib.load().mstar_moe_layer_wait_failures(ctypes.byref(n)), "moe_layer_wait_failures")
+    assert n.value == 0
