@@ -297,3 +297,31 @@ def test_one_launch_opt_out_gives_the_same_layer(tmp_path):
     assert r.returncode == 0, r.stderr[-3000:]
     other = torch.load(tmp_path / "out.pt", weights_only=True)["out"]
     assert torch.equal(out.cpu(), other)
+
+
+@pytest.mark.parametrize("H_,I_,E_,k_,M", [
+    (2048, 768, 64, 4, 33), (2048, 768, 256, 8, 64), (2048, 768, 128, 6, 5),
+    (1024, 384, 128, 8, 1), (1024, 384, 64, 4, 64), (1024, 384, 256, 8, 17)])
+def test_one_launch_layer_sweep_matches_fused_experts(H_, I_, E_, k_, M):
+    """The one-launch decode layer (mstar_moe_layer) at several expert counts,
+    top-k and token counts of the thinker and talker shapes equals
+    fused_experts (two launches, router ids from the layer) bit for bit, and
+    the oracle within tolerance at one point."""
+    from mstar_amd import _lib, ops, quant
+    from mstar_amd.fused_moe import fused_experts
+    g = torch.Generator().manual_seed(H_ + I_ + E_ + k_ + M)
+    w1 = (torch.randn(E_, 2 * I_, H_, generator=g) * 0.02).to(DEV)
+    w2 = (torch.randn(E_, H_, I_, generator=g) * 0.02).to(DEV)
+    q1, s1 = quant.quantize_fp8_block(w1)
+    q2, s2 = quant.quantize_fp8_block(w2)
+    x = torch.randn(M, H_, generator=g).to(torch.bfloat16).to(DEV)
+    logits = torch.randn(M, E_, generator=g).to(DEV)
+    out, tw, ti = ops.moe_layer(x, logits, q1, q2, k_, True, 0, _lib.QUANT_FP8_W8A8, s1, s2)
+    ref = fused_experts(x, q1, q2, tw, ti, quant="fp8_w8a8", w1_scale=s1, w2_scale=s2)
+    assert torch.equal(out, ref)
+    if M == 64:
+        rw, rids = O.router_topk_softmax(logits.cpu(), k_, True)
+        oref = O.fused_experts_rounding(x.cpu(), None, None, rw, rids,
+                                        w1_dq=O.dequant_fp8_block(q1.cpu(), s1.cpu()),
+                                        w2_dq=O.dequant_fp8_block(q2.cpu(), s2.cpu()), act_quant=True)
+        assert_moe_close(out, oref, what=f"one-launch layer H={H_} E={E_} k={k_} M={M}")
