@@ -176,47 +176,53 @@ def layer_kernel_bytes(M, hits):
             + 2 * slots * INTER * 2 + slots * H * 2 + slots * 8)
 
 
-def layer_kernel_timing(x, logits, weights, steps, warmup):
+def layer_kernel_timing(x, logits, weights, steps, warmup, per_graph=20):
     """Mean duration of the decode layer's expert launch alone (gate_up and
     down in one kernel, mstar_moe_stream_layer) on the routing launch's
-    outputs, from HIP events recorded on the stream the kernel is launched on.
-    Every launch gets its own zeroed sync words (allocated before timing)."""
+    outputs.  A HIP graph holds one clear of the sync words (a fill kernel)
+    and `per_graph` launches, each on its own sync words and weight copy; a
+    torch.cuda.Event pair on the launch stream brackets each replay, and the
+    result is the replay time / per_graph (the fill adds ~2 us / per_graph)."""
     from mstar_amd import _lib
     lib = _lib.load()
     M = x.shape[0]
     dev = x.device
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
     slots = M * K_TOP
     tw = torch.empty(slots, dtype=torch.float32, device=dev)
     ti = torch.empty(slots, dtype=torch.int32, device=dev)
     hq = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
     hs = torch.empty(M, H // 128, dtype=torch.float32, device=dev)
+    sp0 = torch.cuda.current_stream().cuda_stream
     _lib.check(lib.mstar_moe_topk_softmax_quant(
         logits.data_ptr(), _lib.DT_F32, M, E, K_TOP, 1, tw.data_ptr(), ti.data_ptr(), None,
-        x.data_ptr(), H, hq.data_ptr(), hs.data_ptr(), sp), "topk_softmax_quant")
+        x.data_ptr(), H, hq.data_ptr(), hs.data_ptr(), sp0), "topk_softmax_quant")
     act = torch.empty(slots, INTER, dtype=torch.bfloat16, device=dev)
     rows = torch.empty(slots, H, dtype=torch.bfloat16, device=dev)
-    sync = torch.zeros(warmup + steps, E + 1, dtype=torch.int32, device=dev)
+    sync = torch.zeros(per_graph, E + 1, dtype=torch.int32, device=dev)
 
-    def launch(i, w):
-        q1, s1, q2, s2 = w
-        _lib.check(lib.mstar_moe_stream_layer(
-            hq.data_ptr(), hs.data_ptr(), q1.data_ptr(), s1.data_ptr(), q2.data_ptr(), s2.data_ptr(),
-            tw.data_ptr(), ti.data_ptr(), M, H, E, INTER, K_TOP, 0, act.data_ptr(), rows.data_ptr(),
-            sync[i].data_ptr(), sp), "moe_stream_layer")
+    def launches():
+        sync.zero_()
+        sp = torch.cuda.current_stream().cuda_stream
+        for i in range(per_graph):
+            q1, s1, q2, s2 = weights[i % len(weights)]
+            _lib.check(lib.mstar_moe_stream_layer(
+                hq.data_ptr(), hs.data_ptr(), q1.data_ptr(), s1.data_ptr(), q2.data_ptr(), s2.data_ptr(),
+                tw.data_ptr(), ti.data_ptr(), M, H, E, INTER, K_TOP, 0, act.data_ptr(), rows.data_ptr(),
+                sync[i].data_ptr(), sp), "moe_stream_layer")
 
-    for i in range(warmup):
-        launch(i, weights[i % len(weights)])
-    # An event pair around every launch: host gaps between launches stay out.
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    g, _ = capture(launches)
+    stream = torch.cuda.current_stream()
+    for _ in range(max(1, warmup // per_graph)):
+        g.replay()
+    reps = max(1, steps // per_graph)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     torch.cuda.synchronize()
-    for i in range(steps):
-        ev[i][0].record(stream)
-        launch(warmup + i, weights[i % len(weights)])
-        ev[i][1].record(stream)
+    for a, b in ev:
+        a.record(stream)
+        g.replay()
+        b.record(stream)
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in ev) * 1e3 / steps  # us
+    return sum(a.elapsed_time(b) for a, b in ev) * 1e3 / (reps * per_graph)  # us
 
 
 def dense_fp8_lines(args, K=2048):
@@ -466,7 +472,7 @@ def main():
                    "layers_per_step": W_COPIES},
         "layer": {"us": round(us, 2), "single_graph_us": round(single_us, 2), "algorithmic_bytes": layer_bytes, "GBps": round(layer_gbs, 1),
                   "hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
-        "roofline": {"kernel": "stream_fp8_layer_kernel (gate_up + SiLU-and-mul, then down x routed weight)",
+        "roofline": {"kernel": "stream_layer_kernel<16, 6, false> (gate_up + SiLU-and-mul, then down x routed weight)",
                      "bound": "hbm",
                      "achieved": round(g1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g1_gbs / HBM_PEAK_GBS, 4),
