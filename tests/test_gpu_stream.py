@@ -325,3 +325,38 @@ def test_one_launch_layer_sweep_matches_fused_experts(H_, I_, E_, k_, M):
                                         w1_dq=O.dequant_fp8_block(q1.cpu(), s1.cpu()),
                                         w2_dq=O.dequant_fp8_block(q2.cpu(), s2.cpu()), act_quant=True)
         assert_moe_close(out, oref, what=f"one-launch layer H={H_} E={E_} k={k_} M={M}")
+
+
+@pytest.mark.parametrize("quant", ["fp8_w8a8", "w4a16"])
+def test_one_launch_layer_gelu(quant):
+    """The one-launch decode layer with the GeLU-and-mul gate (activation 1)
+    equals fused_experts(activation="gelu") on the layer's own routing bit for
+    bit (FP8 and W4A16 weights, M=32 at the thinker shape), and the FP8 layer
+    meets the oracle's GeLU layer within tolerance."""
+    from mstar_amd import _lib, ops, quant as Q
+    from mstar_amd.fused_moe import fused_experts
+    H_, I_, E_, k_, M = 2048, 768, 128, 8, 32
+    g = torch.Generator().manual_seed(91)
+    w1 = (torch.randn(E_, 2 * I_, H_, generator=g) * 0.02).to(DEV)
+    w2 = (torch.randn(E_, H_, I_, generator=g) * 0.02).to(DEV)
+    if quant == "fp8_w8a8":
+        q1, s1 = Q.quantize_fp8_block(w1)
+        q2, s2 = Q.quantize_fp8_block(w2)
+        qc = _lib.QUANT_FP8_W8A8
+    else:
+        q1, s1 = Q.quantize_int4_group(w1)
+        q2, s2 = Q.quantize_int4_group(w2)
+        qc = _lib.QUANT_W4A16
+    x = torch.randn(M, H_, generator=g).to(torch.bfloat16).to(DEV)
+    logits = torch.randn(M, E_, generator=g).to(DEV)
+    out, tw, ti = ops.moe_layer(x, logits, q1, q2, k_, True, 1, qc, s1, s2)
+    ref = fused_experts(x, q1, q2, tw, ti, "gelu", quant=quant, w1_scale=s1, w2_scale=s2)
+    assert torch.equal(out, ref)
+    silu, _, _ = ops.moe_layer(x, logits, q1, q2, k_, True, 0, qc, s1, s2)
+    assert not torch.equal(out, silu)
+    if quant == "fp8_w8a8":
+        rw, rids = O.router_topk_softmax(logits.cpu(), k_, True)
+        oref = O.fused_experts_rounding(x.cpu(), None, None, rw, rids, activation="gelu",
+                                        w1_dq=O.dequant_fp8_block(q1.cpu(), s1.cpu()),
+                                        w2_dq=O.dequant_fp8_block(q2.cpu(), s2.cpu()), act_quant=True)
+        assert_moe_close(out, oref, what="one-launch layer gelu")
