@@ -85,6 +85,9 @@ def parse():
                         "(for rocprofv3 --pmc runs, which count per dispatch)")
     p.add_argument("--profile-w4", type=int, default=0, metavar="M",
                    help="run the config-5 W4A16 layer at M tokens eagerly --steps times (as above)")
+    p.add_argument("--profile-dense", type=int, default=0, metavar="M",
+                   help="run the config-4 dense W8A8 GEMM (N=151936) at M tokens eagerly --steps times "
+                        "(as above)")
     return p.parse_args()
 
 
@@ -387,6 +390,22 @@ def main():
     from mstar_amd import _lib
     _lib.load()
 
+    if args.profile_dense:
+        from mstar_amd import ops, quant
+        g = torch.Generator(device="cuda").manual_seed(7)
+        wq, ws = quant.quantize_fp8_per_channel(torch.randn(151936, H, generator=g, device="cuda") * 0.02)
+        a = torch.randn(args.profile_dense, H, generator=g, device="cuda").to(torch.bfloat16)
+        aq, sa = ops.quant_fp8_per_token(a)
+        run = lambda: ops.fp8_scaled_mm(aq, sa, wq, ws)
+        run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            run()
+        torch.cuda.synchronize()
+        print(json.dumps({"dense_tokens": args.profile_dense,
+                          "eager_us": (time.perf_counter() - t0) / args.steps * 1e6}))
+        return
     if args.profile_w4:
         from mstar_amd import ops, quant
         g = torch.Generator(device="cuda").manual_seed(9)
