@@ -360,3 +360,41 @@ def test_one_launch_layer_gelu(quant):
                                         w1_dq=O.dequant_fp8_block(q1.cpu(), s1.cpu()),
                                         w2_dq=O.dequant_fp8_block(q2.cpu(), s2.cpu()), act_quant=True)
         assert_moe_close(out, oref, what="one-launch layer gelu")
+
+
+@pytest.mark.parametrize("quant,M", [("w4a16", 64), ("w4a16", 17), ("fp8_w8a8", 64)])
+def test_one_launch_layer_skewed_routing(quant, M):
+    """Every token routed to the same 8 experts (M rows each): both phases of
+    the one-launch layer stage their rows in windows and every down window
+    waits on gate_up work of many workgroups.  Bit-exact against
+    fused_experts on the same routing, and no wait gives up."""
+    import ctypes
+    from mstar_amd import _lib, ops, quant as Q
+    from mstar_amd.fused_moe import fused_experts
+    H_, I_, E_, k_ = 2048, 768, 128, 8
+    g = torch.Generator().manual_seed(200 + M)
+    w1 = (torch.randn(E_, 2 * I_, H_, generator=g) * 0.02).to(DEV)
+    w2 = (torch.randn(E_, H_, I_, generator=g) * 0.02).to(DEV)
+    if quant == "fp8_w8a8":
+        q1, s1 = Q.quantize_fp8_block(w1)
+        q2, s2 = Q.quantize_fp8_block(w2)
+        qc = _lib.QUANT_FP8_W8A8
+    else:
+        q1, s1 = Q.quantize_int4_group(w1)
+        q2, s2 = Q.quantize_int4_group(w2)
+        qc = _lib.QUANT_W4A16
+    x = torch.randn(M, H_, generator=g).to(torch.bfloat16).to(DEV)
+    logits = torch.randn(M, E_, generator=g)
+    logits[:, 40:48] += 50.0  # experts 40-47 win for every token
+    logits = logits.to(DEV)
+    lib = _lib.load()
+    before = ctypes.c_int(-1)
+    _lib.check(lib.mstar_moe_layer_wait_failures(ctypes.byref(before)), "wait_failures")
+    out, tw, ti = ops.moe_layer(x, logits, q1, q2, k_, True, 0, qc, s1, s2)
+    assert sorted(set(ti.flatten().tolist())) == list(range(40, 48))
+    ref = fused_experts(x, q1, q2, tw, ti, quant=quant, w1_scale=s1, w2_scale=s2)
+    assert torch.equal(out, ref)
+    torch.cuda.synchronize()
+    after = ctypes.c_int(-1)
+    _lib.check(lib.mstar_moe_layer_wait_failures(ctypes.byref(after)), "wait_failures")
+    assert after.value == before.value
