@@ -201,7 +201,9 @@ def layer_kernel_timing(x, logits, weights, steps, warmup, per_graph=20):
         x.data_ptr(), H, hq.data_ptr(), hs.data_ptr(), sp0), "topk_softmax_quant")
     act = torch.empty(slots, INTER, dtype=torch.bfloat16, device=dev)
     rows = torch.empty(slots, H, dtype=torch.bfloat16, device=dev)
-    sync = torch.zeros(per_graph, E + 1, dtype=torch.int32, device=dev)
+    nsync = ctypes.c_int64(0)
+    _lib.check(lib.mstar_moe_layer_sync_words(E, ctypes.byref(nsync)), "layer_sync_words")
+    sync = torch.zeros(per_graph, nsync.value, dtype=torch.int32, device=dev)
 
     def launches():
         sync.zero_()

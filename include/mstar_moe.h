@@ -216,8 +216,13 @@ int mstar_moe_stream_gemm(const void* A, int a_dtype, const float* a_scale, cons
  *   act: bf16 [num_tokens * top_k, inter] scratch (the SiLU-and-mul rows);
  *   out_rows: bf16 [num_tokens * top_k, hidden], each slot's down row times its
  *     routed weight (mstar_moe_sum_reduce gives the layer output);
- *   sync: int32 [num_experts + 1], ZERO when the launch starts (it is not
- *     cleared again; mstar_moe_layer's routing launch clears its own).
+ *   sync: int32 [MSTAR_MOE_LAYER_SYNC_WORDS(num_experts)], ZERO when the
+ *     launch starts (it is not cleared again; mstar_moe_layer's routing
+ *     launch clears its own): per-expert progress counters, an error word
+ *     (sync[num_experts], 1 if a wait gave up) and per-workgroup claim words.
+ * Workgroups claim the gate_up work a down wait depends on before waiting,
+ * so the launch completes whatever share of the CUs it gets; a wait that
+ * still exceeds 100 ms sets the error word and writes NaN rows.
  * Shapes: (hidden, inter) = (2048, 768) or (1024, 384), num_tokens * top_k <= 1024 (otherwise
  * MSTAR_UNSUPPORTED). */
 int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, const float* w1_scale,
@@ -226,15 +231,29 @@ int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, cons
                            int num_experts, int64_t inter, int top_k, int activation, void* act,
                            void* out_rows, int32_t* sync, void* stream);
 
+#define MSTAR_MOE_LAYER_SYNC_WORDS(num_experts) ((((num_experts) + 16) / 16) * 16 + 16 * 1024)
+
+/* The same count as MSTAR_MOE_LAYER_SYNC_WORDS, for bindings that cannot
+ * read the macro.  No counterpart in the reference. */
+int mstar_moe_layer_sync_words(int num_experts, int64_t* words);
+
 /* Number of waits of the one-launch decode layer kernel (mstar_moe_layer at
  * decode sizes, mstar_moe_stream_layer) that gave up on the current device
- * since the library was loaded; a launch with such a wait produced invalid
- * output.  The kernel's workgroups wait on each other, which needs them all
- * resident: never the case while another such launch runs on the device.
- * Setting MSTAR_MOE_ONE_LAUNCH=0 in the environment makes mstar_moe_layer
- * use the two-launch form, which has no such wait.  No counterpart in the
+ * since the library was loaded (synchronous read).  A wait ends by design
+ * (see mstar_moe_stream_layer); one that gave up wrote NaN into the rows of
+ * the experts it waited for, so that launch's output is detectably invalid.
+ * MSTAR_MOE_ONE_LAUNCH=0 in the environment makes mstar_moe_layer use the
+ * two-launch form, which has no waits at all.  No counterpart in the
  * reference (a diagnostic of this library's kernel). */
 int mstar_moe_layer_wait_failures(int* count);
+
+/* Testing hook for the one-launch decode layer: the mode of the launches
+ * enqueued from now on in this process.  0 normal; 1 odd workgroups do not
+ * claim their own gate_up work (as if they were not resident yet), so other
+ * workgroups must take it over; 2 every down-phase wait gives up at once
+ * (the output rows become NaN and the error word is set).  No counterpart in
+ * the reference; for tests only. */
+int mstar_moe_debug_layer_test_mode(int mode);
 
 /* Workspace bytes mstar_fused_moe needs for these sizes. */
 int mstar_fused_moe_workspace_size(int64_t num_tokens, int64_t hidden, int num_experts,

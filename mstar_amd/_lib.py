@@ -65,7 +65,9 @@ SIGNATURES = {
     "mstar_moe_stream_layer": (
         _c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_int, _c_i64, _c_int,
                  _c_int, _vp, _vp, _vp, _vp]),
+    "mstar_moe_layer_sync_words": (_c_int, [_c_int, ctypes.POINTER(_c_i64)]),
     "mstar_moe_layer_wait_failures": (_c_int, [ctypes.POINTER(_c_int)]),
+    "mstar_moe_debug_layer_test_mode": (_c_int, [_c_int]),
     "mstar_fused_moe_workspace_size": (
         _c_int, [_c_i64, _c_i64, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int,
                  ctypes.POINTER(ctypes.c_size_t)]),

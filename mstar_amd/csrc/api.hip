@@ -163,7 +163,7 @@ static int make_plan(int64_t M, int64_t H, int E, int64_t I, int top_k, int quan
   pl->one_launch = one_launch_enabled() && with_route && pl->ids_mode && pl->stream && reduce &&
                    (pl->route_quant || quant == MSTAR_QUANT_W4A16) &&
                    stream_layer_supported(H, I, pl->slots, E, quant == MSTAR_QUANT_W4A16);
-  pl->off_sync = pl->one_launch ? take((size_t)(E + 1) * 4) : 0;
+  pl->off_sync = pl->one_launch ? take((size_t)layer_sync_words(E, kLayerSyncMaxCus) * 4) : 0;
   pl->off_hq = fp8_tiled ? take((size_t)M * H) : pl->route_quant ? take((size_t)M * H * 2) : 0;
   pl->off_hs = fp8_tiled || pl->route_quant ? take((size_t)M * (H / 128) * 4) : 0;
   const size_t cq_rows = pl->by_pos ? pos_rows : (size_t)pl->slots;
@@ -446,6 +446,17 @@ int mstar_moe_stream_layer(const void* hq, const float* hs, const void* w1, cons
 
 int mstar_moe_layer_wait_failures(int* count) { return layer_wait_failures(count); }
 
+int mstar_moe_layer_sync_words(int num_experts, int64_t* words) {
+  if (num_experts <= 0 || num_experts > 1024 || !words) {
+    set_last_error("moe_layer_sync_words: invalid arguments (E=%d)", num_experts);
+    return kInvalidArgument;
+  }
+  *words = layer_sync_words(num_experts, kLayerSyncMaxCus);
+  return kOk;
+}
+
+int mstar_moe_debug_layer_test_mode(int mode) { return set_layer_test_mode(mode); }
+
 int mstar_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
                                int num_experts, int block_size, int32_t* sorted_token_ids,
                                int64_t sorted_len, int32_t* expert_ids, int64_t expert_ids_len,
@@ -512,7 +523,9 @@ int mstar_fp8_scaled_mm(const uint8_t* a, const float* a_scale, const uint8_t* w
     // 256-row tiles, or 128-row tiles when the 256-row ones would not give
     // every CU a tile (N=2048 at M=4096: 128 tiles of 256 rows for 256 CUs).
     const int64_t tiles256 = ((M + kBigBlockM - 1) / kBigBlockM) * ((N + 255) / 256);
-    const int bm = tiles256 < device_cu_count() ? kBigBlockM / 2 : kBigBlockM;
+    const int cus = device_cu_count();
+    if (cus <= 0) return kLaunchError;
+    const int bm = tiles256 < cus ? kBigBlockM / 2 : kBigBlockM;
     return launch_gemm_fp8_big(g, EPI_DENSE, false, bm, (hipStream_t)stream);
   }
   return launch_tile_gemm(g, A_FP8R, B_FP8R, EPI_DENSE, kBF16, false, M <= 32 ? 32 : 64,
@@ -661,17 +674,28 @@ int mstar_moe_layer_workspace_size(int64_t num_tokens, int64_t hidden, int num_e
   return st;
 }
 
-int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
-                    const void* router_logits, int logits_dtype, int renormalize, const void* w1,
-                    const void* w2, int num_experts, int64_t inter, int quant,
-                    const void* w1_scale, const void* w2_scale, int top_k, int activation,
-                    void* out, float* topk_weights_out, int64_t* topk_ids_out, void* workspace,
-                    size_t workspace_bytes, void* stream_) {
+extern "C++" {
+namespace mstar {
+// mstar_moe_layer; allow_one_launch = false keeps the decode layer in its
+// two-launch form (no sync words, no waits between workgroups).
+int moe_layer_impl(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                   const void* router_logits, int logits_dtype, int renormalize, const void* w1,
+                   const void* w2, int num_experts, int64_t inter, int quant,
+                   const void* w1_scale, const void* w2_scale, int top_k, int activation,
+                   void* out, float* topk_weights_out, int64_t* topk_ids_out, void* workspace,
+                   size_t workspace_bytes, void* stream_, bool allow_one_launch) {
   hipStream_t stream = (hipStream_t)stream_;
   Plan pl;
   int st = make_plan(num_tokens, hidden_size, num_experts, inter, top_k, quant, act_dtype, 1, &pl,
                      true);
   if (st != kOk) return st;
+  if (!allow_one_launch) pl.one_launch = false;
+  int sync_clear = 0;
+  if (pl.one_launch) {
+    const int cus = device_cu_count();
+    if (cus <= 0) return kLaunchError;
+    sync_clear = layer_sync_words(num_experts, cus < kLayerSyncMaxCus ? cus : kLayerSyncMaxCus);
+  }
   if ((st = check_layer_args(pl, activation, workspace, workspace_bytes)) != kOk) return st;
   if (num_tokens == 0) return kOk;
   if (!hidden || !router_logits || !w1 || !w2 || !out ||
@@ -687,8 +711,7 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
                              renormalize, tw, ids32, topk_ids_out, stream,
                              pl.route_quant ? hidden : nullptr, hidden_size,
                              (uint16_t*)(ws + pl.off_hq), (float*)(ws + pl.off_hs),
-                             pl.one_launch ? (int*)(ws + pl.off_sync) : nullptr,
-                             pl.one_launch ? num_experts + 1 : 0);
+                             pl.one_launch ? (int*)(ws + pl.off_sync) : nullptr, sync_clear);
   else
     st = launch_route(router_logits, logits_dtype, num_tokens, num_experts, top_k, renormalize, tw,
                       ids32, topk_ids_out, pl.bm, (int32_t*)(ws + pl.off_sorted),
@@ -701,6 +724,20 @@ int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64
   return run_experts(pl, hidden, act_dtype, num_tokens, hidden_size, w1, w2, num_experts, inter,
                      quant, w1_scale, w2_scale, tw, kF32, ids32, kI32, top_k, activation, 1, out,
                      ws, stream);
+}
+}  // namespace mstar
+}  // extern "C++"
+
+int mstar_moe_layer(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                    const void* router_logits, int logits_dtype, int renormalize, const void* w1,
+                    const void* w2, int num_experts, int64_t inter, int quant,
+                    const void* w1_scale, const void* w2_scale, int top_k, int activation,
+                    void* out, float* topk_weights_out, int64_t* topk_ids_out, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  return moe_layer_impl(hidden, act_dtype, num_tokens, hidden_size, router_logits, logits_dtype,
+                        renormalize, w1, w2, num_experts, inter, quant, w1_scale, w2_scale, top_k,
+                        activation, out, topk_weights_out, topk_ids_out, workspace, workspace_bytes,
+                        stream, true);
 }
 
 int mstar_moe_block(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,

@@ -179,6 +179,7 @@ bool dense_stream_supported(int64_t M, int64_t N, int64_t K) {
 template <int MS, int RING, int KC>
 static int run_dense_stream(const GemmArgs& a, hipStream_t stream) {
   const int cus = device_cu_count();
+  if (cus <= 0) return kLaunchError;
   const int items = a.N / 16;
   const int per = (items + cus - 1) / cus;
   const size_t shmem = ds_lds_bytes(RING, KC, MS, a.K);

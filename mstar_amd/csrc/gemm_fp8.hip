@@ -653,6 +653,7 @@ static int run_big(const GemmArgs& a, hipStream_t stream) {
   if (st != kOk) return st;
   // Persistent: one workgroup per CU (the LDS ring allows no more).
   const int64_t grid = device_cu_count();
+  if (grid <= 0) return kLaunchError;
   kern<<<dim3((unsigned)grid), dim3(kBigThreads), lds, stream>>>(a);
   return launch_status("gemm_fp8_big");
 }

@@ -364,6 +364,7 @@ static int run_w4_tile(const GemmArgs& a, const float* xs, float* xs_out, hipStr
   if (st != kOk) return st;
   // Persistent: one workgroup per CU (the LDS ring allows no more).
   const int cus = device_cu_count();
+  if (cus <= 0) return kLaunchError;
   if (a.m_blocks == 0) return kOk;
   kern<<<dim3((unsigned)cus), dim3(kW4Threads), kW4Lds, stream>>>(a, xs, xs_out);
   return launch_status("w4_tile");

@@ -9,13 +9,15 @@
 namespace mstar {
 
 // launch_state.hip: per-device launch state, safe from several host threads.
-// CU count of the current device (cached per device).
+// CU count of the current device (cached per device); 0 with the error
+// message set if the device cannot be read (hipGetDevice failing).
 int device_cu_count();
 // Opt `kernel` into `bytes` of dynamic LDS on the current device (once per
 // device and size); kOk or kLaunchError with the message set.
 int ensure_dynamic_lds(const void* kernel, size_t bytes, const char* what);
 // Resident workgroups per CU of `kernel` at this block size and LDS size on
-// the current device (cached per device, kernel, block size and LDS size).
+// the current device (cached per device, kernel, block size and LDS size);
+// 0 with the error message set if the device cannot be read.
 int occupancy_per_cu(const void* kernel, int threads, size_t lds_bytes);
 
 // route.hip
@@ -174,10 +176,24 @@ int launch_stream_fp8(const GemmArgs& a, int epi, bool exact, hipStream_t stream
 constexpr int64_t kStreamMaxIdsSlots = 1024;  // slots a launch in ids mode can take
 // The decode layer's gate_up and down streaming GEMMs in one launch (g1:
 // gate_up on the routing launch's widened FP8 token rows, or int4 on bf16
-// hidden rows; g2: down on g1's bf16 output).  sync_words: E + 1 ints, zero
-// when the launch starts (the routing launch clears them).
+// hidden rows; g2: down on g1's bf16 output).  sync_words: at least
+// layer_sync_words(E, CU count) ints, zero when the launch starts (the
+// routing launch clears them).
 bool stream_layer_supported(int64_t H, int64_t I, int64_t slots, int E, bool int4);
 int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* sync_words, hipStream_t stream);
+// Sync words a layer launch of `nwg` workgroups reads (per-expert counters,
+// the error word, per-range claim words).
+int layer_sync_words(int E, int nwg);
+constexpr int kLayerSyncMaxCus = 1024;
+// Test hook: the mode of the layer launches enqueued from now on.
+int set_layer_test_mode(int mode);
+// mstar_moe_layer with the one-launch decode layer allowed or not.
+int moe_layer_impl(const void* hidden, int act_dtype, int64_t num_tokens, int64_t hidden_size,
+                   const void* router_logits, int logits_dtype, int renormalize, const void* w1,
+                   const void* w2, int num_experts, int64_t inter, int quant,
+                   const void* w1_scale, const void* w2_scale, int top_k, int activation,
+                   void* out, float* topk_weights_out, int64_t* topk_ids_out, void* workspace,
+                   size_t workspace_bytes, void* stream, bool allow_one_launch);
 // Waits of the layer kernel that gave up on the current device (synchronous copy).
 int layer_wait_failures(int* count);
 bool stream_fp8_supported(int K, int N, int inter, int epi);

@@ -81,7 +81,10 @@ extern "C" int mstar_moe_layer_noalloc(const void* hidden, int act_dtype, int64_
   }
   void* ws = scratch_ptr();
   if (!ws) return kLaunchError;
-  return mstar_moe_layer(hidden, act_dtype, num_tokens, hidden_size, router_logits, logits_dtype,
-                         renormalize, w1, w2, num_experts, inter, quant, w1_scale, w2_scale, top_k,
-                         activation, out, topk_weights_out, topk_ids_out, ws, kScratchBytes, stream);
+  // The two-launch decode form: the one-launch kernel's sync words would sit
+  // in the shared array, where overlapping calls would reset each other's.
+  return moe_layer_impl(hidden, act_dtype, num_tokens, hidden_size, router_logits, logits_dtype,
+                        renormalize, w1, w2, num_experts, inter, quant, w1_scale, w2_scale, top_k,
+                        activation, out, topk_weights_out, topk_ids_out, ws, kScratchBytes, stream,
+                        false);
 }

@@ -26,8 +26,11 @@
 // and up rows of one output column sit in lanes l and l+8), or the down
 // projection times the routed weight into [slots, H] (the reference's
 // fused_moe_kernel with MUL_ROUTED_WEIGHT, kernels.py:129-138).
+#include <atomic>
+
 #include "common.h"
 #include "launch.h"
+#include "layer_sync.h"
 
 namespace mstar {
 
@@ -394,12 +397,18 @@ template <int KS, bool W4 = false>
 __host__ __device__ constexpr size_t cu_ring_bytes() {
   return (size_t)cu_waves<W4>() * kCuRing * (W4 ? cu_w4_slot<KS>() : cu_kc<KS>() * 2048);
 }
-// LDS layout: rings | sAct[E] sCnt[E] sOff[E] sList[M'] sMask[32] | sSc[cap][KS]
-// sRw[cap] | rows[cap][pitch].  The lists sit at the same offset for every KS
+// LDS layout: rings | sAct[E] sCnt[E] sOff[E] sList[M'] sMask[32] sFlags[kFlagWords]
+// | sSc[cap][KS] sRw[cap] | rows[cap][pitch].  The lists sit at the same offset for every KS
 // with the same ring size, so the layout kernel's down phase reuses the
 // gate_up phase's lists.
+// sFlags (the layer kernel's per-workgroup words): [0] the workgroup's own
+// gate_up range is its to run, [1] the current down window's wait gave up,
+// [2] ranges stolen, [3 ..) their indices.
+constexpr int kFlagOwn = 0, kFlagPoison = 1, kFlagStealN = 2, kFlagSteal = 3;
+constexpr int kMaxSteals = 256;
+constexpr int kFlagWords = kFlagSteal + kMaxSteals + 1;
 __host__ __device__ inline size_t cu_lists_bytes(int E, int64_t M) {
-  return ((size_t)3 * E + (size_t)((M + 3) & ~3ll) + 32) * 4;
+  return ((size_t)3 * E + (size_t)((M + 3) & ~3ll) + 32 + kFlagWords) * 4;
 }
 template <int KS, bool W4 = false>
 __host__ __device__ inline size_t cu_sc_off(int E, int64_t M, size_t lists_at = 0) {
@@ -463,22 +472,60 @@ __device__ uint64_t g_timeline[2 * 1024 * 8];  // [EPI][workgroup][phase]
 // finished; the down phase stages an expert's activation rows only once
 // all of that expert's gate_up pairs are reported.
 enum : int { kPhaseAlone = 0, kPhaseGate = 1, kPhaseDown = 2 };
+//
+// Forward progress.  Gate_up range q belongs to whichever workgroup first
+// claims it: claim word q goes 0 -> 1 (its own workgroup, at its start) or
+// 0 -> 2 (a thief).  At the end of its own gate_up phase every workgroup
+// tries to claim each gate_up range its down range depends on and runs the
+// ones it wins before its down phase.  So before any down-phase wait, every
+// range the wait depends on is claimed by a workgroup that is running and
+// whose gate_up work never waits: every wait ends, even when some of the
+// launch's workgroups are not resident (another kernel or process holds CUs)
+// -- the late ones find their ranges taken and go straight to their down
+// work.  A wait longer than kLayerWaitTicks is therefore a fault, not a
+// schedule: it sets *err, counts itself and writes NaN rows for the window it
+// gave up on, so the output is detectably invalid, never silently wrong.
+enum : int { kLayerNormal = 0, kLayerTestNoOwnClaim = 1, kLayerTestGiveUp = 2 };
 struct LayerSync {
   int* done;       // [E] gate_up (item, token row) pairs finished per expert; zero at launch
   int* err;        // set to 1 if a wait gave up (output of that launch invalid)
+  int* claim;      // claim word of gate_up range q at claim[q * kClaimStride]; zero at launch
   int gate_ipe;    // gate_up items per expert (inter / 8)
+  int down_ipe;    // down items per expert (hidden / 16)
   int lists_at;    // LDS offset of the expert lists (after both phases' rings)
+  int mode;        // kLayerNormal, or a test mode set from the host:
+                   // kLayerTestNoOwnClaim: odd workgroups do not claim their own range
+                   // (as if not yet resident), kLayerTestGiveUp: every wait gives up at once
 };
+constexpr int kClaimStride = 16;  // one claim word per 64 bytes
+constexpr int kMaxLayerRanges = kLayerSyncMaxCus;  // workgroups of a layer launch (one per CU)
+// Sync words: done[E], err, then the claim words from a 16-word boundary.
+__host__ __device__ inline int layer_claim_base(int E) { return (E + 16) / 16 * 16; }
+int layer_sync_words(int E, int nwg) { return layer_claim_base(E) + kClaimStride * nwg; }
+// Test mode of the launches enqueued from now on (mstar_moe_debug_layer_test_mode).
+static std::atomic<int> g_layer_test_mode{kLayerNormal};
+int set_layer_test_mode(int mode) {
+  if (mode != kLayerNormal && mode != kLayerTestNoOwnClaim && mode != kLayerTestGiveUp) {
+    set_last_error("moe_debug_layer_test_mode: unknown mode %d", mode);
+    return kInvalidArgument;
+  }
+  g_layer_test_mode.store(mode, std::memory_order_relaxed);
+  return kOk;
+}
 // Waits of the layer kernel that gave up (kLayerWaitTicks), on this device,
 // since the library was loaded: read by mstar_moe_layer_wait_failures.
 __device__ int g_layer_wait_failures;
 // Longest wait of the down phase for an expert's gate_up rows before it
-// gives up (s_memrealtime ticks of 10 ns): 20 ms.
-constexpr uint64_t kLayerWaitTicks = 2000000;
+// gives up (s_memrealtime ticks of 10 ns): 100 ms.
+constexpr uint64_t kLayerWaitTicks = 10000000;
 
 // One workgroup's share of a streaming GEMM: work range `wg` of `nwg`.
+// Layer gate_up phase: `own` -- range wg is this workgroup's own (claimed
+// here; the end of the phase also claims the ranges its down range waits
+// on), else a range it already claimed as a thief.
 template <int EPI, int KS, int STAGE, int PHASE = kPhaseAlone>
-__device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int wg, int nwg, const LayerSync& ls) {
+__device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int wg, int nwg, const LayerSync& ls,
+                                               bool own = true) {
   static_assert(PHASE == kPhaseAlone || (PHASE == kPhaseGate) == (EPI == EPI_ACT),
                 "layer phases: gate_up, then down");
   constexpr bool W4 = STAGE == STAGE_W4;
@@ -513,6 +560,7 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
   float* sRw = sSc + cap * KS;  // routed weight of each staged row
   uint8_t* sRows = smem + cu_rows_off<KS, W4>(E, p.M, cap, lists_at);
   uint32_t* sMask = (uint32_t*)(sList + ((p.M + 3) & ~3ll));  // [32] active experts (E <= 1024)
+  int* sFlags = (int*)(sMask + 32);
   // The down phase of the layer kernel finds the lists the gate_up phase
   // built from the same router ids.
   constexpr bool kListsBuilt = PHASE == kPhaseDown;
@@ -527,22 +575,46 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
   MSTAR_TL(0);
   // ---- prologue 1: per-expert counts and the active-expert mask.
   int my_e[SPT], my_pos[SPT];
+  // Layer gate_up phase: the last wave (the one with the fewest items)
+  // claims the own range (0 -> 1) once its router ids have arrived, so that
+  // no wait of the prologue waits for it; its answer is read after the
+  // wave's first weight chunk.
+  constexpr int CW = NWV - 1;
+  int own_old = 1;
   if constexpr (!kListsBuilt) {
+    // All of a thread's id loads in flight at once (one round trip): buffer
+    // loads, which return 0 past the ids without a branch around them.
+    const bool i64 = p.ids_dtype == kI64;
+    const auto rs_ids = make_rsrc(p.topk_ids, (uint32_t)(p.M * (i64 ? 8 : 4)));
+    int lo[SPT], hi[SPT];
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      const uint32_t i = (uint32_t)(tid + j * NTH);
+      lo[j] = __builtin_amdgcn_raw_buffer_load_b32(rs_ids, i64 ? i * 8 : i * 4, 0, 0);
+      hi[j] = i64 ? __builtin_amdgcn_raw_buffer_load_b32(rs_ids, i * 8 + 4, 0, 0) : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      const int i = tid + j * NTH;
+      // Out-of-range ids (negative or >= E, or a high word set) are skipped (.cu:44-46).
+      const bool ok = i < p.M && lo[j] >= 0 && lo[j] < E && (i64 ? hi[j] == 0 : true);
+      my_e[j] = ok ? lo[j] : -1;
+      my_pos[j] = 0;
+    }
+    if constexpr (PHASE == kPhaseGate) {
+      if (own && w == CW && lane == 0 && !(ls.mode == kLayerTestNoOwnClaim && (blockIdx.x & 1))) {
+        own_old = 0;
+        __hip_atomic_compare_exchange_strong(ls.claim + wg * kClaimStride, &own_old, 1, __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
     for (int e = tid; e < E; e += NTH) sCnt[e] = 0;
     if (tid < 32) sMask[tid] = 0;
     MSTAR_TL(1);
     lds_sync();
 #pragma unroll
     for (int j = 0; j < SPT; ++j) {
-      const int i = tid + j * NTH;
-      int e = -1;
-      if (i < p.M) {
-        const int64_t v = p.ids_dtype == kI64 ? ((const int64_t*)p.topk_ids)[i]
-                                              : (int64_t)((const int32_t*)p.topk_ids)[i];
-        e = (v >= 0 && v < E) ? (int)v : -1;  // out-of-range ids are skipped (.cu:44-46)
-      }
-      my_e[j] = e;
-      my_pos[j] = 0;
+      const int e = my_e[j];
       if (e >= 0) {
         my_pos[j] = atomicAdd(&sCnt[e], 1);
         atomicOr(&sMask[e >> 5], 1u << (e & 31));
@@ -557,8 +629,8 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
   const int n_act = wave_last(wincl);
   const int total = n_act * IPE;
   const int T = (total + nwg - 1) / nwg;
-  const int i0 = wg * T;
-  const int i1 = i0 + T < total ? i0 + T : total;
+  int i0 = wg * T;
+  int i1 = i0 + T < total ? i0 + T : total;
   // Without work a workgroup is done, except that the gate_up phase of the
   // layer kernel still builds the lists for its down phase.
   if (i0 >= i1 && PHASE != kPhaseGate) return;
@@ -670,14 +742,54 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
         n += __builtin_popcountll(b);
       }
     }
+    if (PHASE == kPhaseGate && w == 0 && lane == 0) sFlags[kFlagOwn] = 1;  // until told otherwise
     lds_sync();
 #pragma unroll
     for (int j = 0; j < SPT; ++j)
       if (my_e[j] >= 0) sList[sOff[my_e[j]] + my_pos[j]] = tid + j * NTH;
     lds_sync();
   }
-  if (PHASE == kPhaseGate && i0 >= i1) return;
-  const int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
+  // Layer gate_up phase, own range: if another workgroup took the range
+  // first (the answer to the last wave's claim, published after its first
+  // chunk), sFlags[kFlagOwn] is cleared, which every wave checks before each
+  // unit: a late start stops within a unit; rows written meanwhile get the
+  // same values from the taker, and only the taker reports them.  At the end
+  // of its items the last wave claims the other gate_up ranges its down
+  // range waits on (0 -> 2): by then every resident workgroup has claimed
+  // its own.
+  bool own_pending = PHASE == kPhaseGate && own;
+  // The answers -> sFlags: whether the own range is this workgroup's, and
+  // the ranges it took.
+  auto claim_dependencies = [&]() {
+    if constexpr (PHASE == kPhaseGate) {
+      if (!own || w != CW) return;
+      int dep_lo, dep_hi;
+      layer_dependencies(n_act, IPE, ls.down_ipe, nwg, wg, &dep_lo, &dep_hi);
+      int nst = 0;
+      for (int qb = dep_lo; qb <= dep_hi && nst < kMaxSteals; qb += 64) {
+        const int q = qb + lane;
+        int old = 1;
+        if (q <= dep_hi && q != wg) {
+          old = 0;
+          __hip_atomic_compare_exchange_strong(ls.claim + q * kClaimStride, &old, 2, __ATOMIC_RELAXED,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const uint64_t won = __ballot(old == 0);
+        const int before = __builtin_popcountll(won & ((1ull << lane) - 1ull));
+        if (old == 0 && nst + before < kMaxSteals) sFlags[kFlagSteal + nst + before] = q;
+        nst += __builtin_popcountll(won);
+      }
+      if (lane == 0) {
+        const int z = sFlags[kFlagOwn] - 1;  // 0, or -1 if already cleared (own_old != 0 then)
+        sFlags[kFlagOwn] = (own_old | z) == 0;
+        sFlags[kFlagStealN] = nst < kMaxSteals ? nst : kMaxSteals;
+      }
+    }
+  };
+  // The layer's gate_up phase runs its own range, then the ranges it took
+  // over (passes).
+  bool run_pass = PHASE != kPhaseGate || i0 < i1;
+  int a_first = i0 / IPE, a_last = (i1 - 1) / IPE;
   MSTAR_TL(3);
 
   // ---- staging (waves < SW): `nrows` rows; row j reads A row arow_of(j).
@@ -824,6 +936,8 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
   };
 
   bool use_prefetch = prefetched;
+  bool poison = false;  // down phase: the window's wait gave up (NaN rows)
+  int pass = 0;  // gate_up passes: the own range, then ranges taken over
   auto run_window = [&](int lbase) {
     Cur ic, cc;  // issue / compute cursors
     bool ihas = first_unit(i0 + w, ic);
@@ -872,6 +986,9 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
     int cslot = 0;
     while (true) {
       // ---- unit set-up (compute side)
+      if constexpr (PHASE == kPhaseGate) {
+        if (pass == 0 && !__builtin_amdgcn_readfirstlane(sFlags[kFlagOwn])) return;  // the range was taken
+      }
       const int a = cc.it / IPE, g = cc.it - a * IPE;
       const int e = __builtin_amdgcn_readfirstlane(sAct[a]);
       const int off = __builtin_amdgcn_readfirstlane(sOff[e]);
@@ -908,6 +1025,16 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
         // fewer, for the epilogue store / routed-weight load that may sit
         // between them: over-waiting is safe).
         wait_leaving_chunks<DPC, RING>(ahead);
+        if constexpr (PHASE == kPhaseGate) {
+          if (w == CW && own_pending) {  // the claim's answer: older than this chunk's DMA
+            own_pending = false;
+            // z is 0 (sFlags[kFlagOwn] is still 1: this wave is its only
+            // writer); folding it in keeps the compiler from testing the
+            // answer -- and so waiting for it -- right after the claim.
+            const int z = sFlags[kFlagOwn] - 1;
+            if (lane == 0 && (own_old | z) != 0) sFlags[kFlagOwn] = 0;
+          }
+        }
         const uint8_t* wslot = ring + cslot * SLOT;
         // Wave-uniform, so the weight-scale reads below are scalar loads (a
         // vector load here would make the compiler drain the DMA queue).
@@ -995,10 +1122,11 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
           } else {
             if (tok_ok) {
               const float rw = p.mul_routed ? sRw[lrow] : 1.f;
-              const uint32_t lo = (uint32_t)f32_to_bf16_bits(acc[0] * rw) |
-                                  ((uint32_t)f32_to_bf16_bits(acc[1] * rw) << 16);
-              const uint32_t hi = (uint32_t)f32_to_bf16_bits(acc[2] * rw) |
-                                  ((uint32_t)f32_to_bf16_bits(acc[3] * rw) << 16);
+              uint32_t lo = (uint32_t)f32_to_bf16_bits(acc[0] * rw) |
+                            ((uint32_t)f32_to_bf16_bits(acc[1] * rw) << 16);
+              uint32_t hi = (uint32_t)f32_to_bf16_bits(acc[2] * rw) |
+                            ((uint32_t)f32_to_bf16_bits(acc[3] * rw) << 16);
+              if (PHASE == kPhaseDown && poison) lo = hi = 0x7fc07fc0u;  // bf16 NaN: the wait gave up
               *(uint2*)(C + (int64_t)slot_id * p.ldc + g * 16 + 4 * lg) = make_uint2(lo, hi);
             }
           }
@@ -1009,9 +1137,10 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
     }
   };
 
+  for (;; ++pass) {
   // Windows over the CU's experts: as many whole experts as fit in `cap`
   // rows, or `cap` rows of one larger expert.  Usually a single window.
-  int a = a_first, r = 0;
+  int a = run_pass ? a_first : a_last + 1, r = 0;
   bool first_window = true;
   while (a <= a_last) {
     wa0 = a;
@@ -1043,21 +1172,31 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
       // microsecond: every poll is a memory request that competes with the
       // weight streams), then the staging waves acquire their stores.
       if (w == 0) {
+        bool gave_up = false;
         for (int aa = wa0 + lane; aa <= wa1; aa += 64) {
           const int e = sAct[aa];
           const int target = ls.gate_ipe * sCnt[e];
           const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
           while (__hip_atomic_load(ls.done + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (__builtin_amdgcn_s_memrealtime() - t0 > kLayerWaitTicks) {
-              __hip_atomic_store(ls.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              __hip_atomic_fetch_add(&g_layer_wait_failures, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (ls.mode == kLayerTestGiveUp || __builtin_amdgcn_s_memrealtime() - t0 > kLayerWaitTicks) {
+              gave_up = true;
               break;
             }
             __builtin_amdgcn_s_sleep(32);
           }
+          if (ls.mode == kLayerTestGiveUp) gave_up = true;
+        }
+        const bool any = __ballot(gave_up) != 0;
+        if (lane == 0) {
+          sFlags[kFlagPoison] = any;
+          if (any) {
+            __hip_atomic_store(ls.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(&g_layer_wait_failures, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
       }
       lds_sync();  // the staging reads the rows as agent-scope atomics (load_rows16)
+      poison = __builtin_amdgcn_readfirstlane(sFlags[kFlagPoison]) != 0;
     }
     if (w < SW) {
       const auto arow_of = [&](int j) { return sList[lbase + j] / p.top_k; };
@@ -1073,16 +1212,20 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
     run_window(lbase);
     MSTAR_TL(5);
   }
+  if (pass == 0) claim_dependencies();
   wait_vmcnt<0>();  // no DMA outlives the kernel
   MSTAR_TL(7);
-  if constexpr (PHASE == kPhaseGate) {
+  if constexpr (PHASE != kPhaseGate) {
+    break;
+  } else {
     // Report this range's (item, row) pairs per expert once every wave's
     // stores are complete (the wait above): one lane per expert adds
     // (items of the expert in [i0, i1)) x (its rows).  The activation rows
     // were stored as agent-scope atomics, which are coherent across XCDs
     // without the L2 write-back an agent-scope release fence costs.
-    lds_sync();
-    if (w == 0) {
+    lds_sync();  // also: the list of ranges taken over is written
+    // Only the range's claimant reports it.
+    if (w == 0 && run_pass && (pass > 0 || sFlags[kFlagOwn])) {
       for (int a = a_first + lane; a <= a_last; a += 64) {
         const int lo = i0 > a * IPE ? i0 : a * IPE;
         const int hi = i1 < (a + 1) * IPE ? i1 : (a + 1) * IPE;
@@ -1090,6 +1233,16 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
         __hip_atomic_fetch_add(ls.done + e, (hi - lo) * sCnt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+    // Next pass: a range taken over (claimed, with items, by construction).
+    if (!own || pass >= __builtin_amdgcn_readfirstlane(sFlags[kFlagStealN])) break;
+    const int q = __builtin_amdgcn_readfirstlane(sFlags[kFlagSteal + pass]);
+    i0 = q * T;
+    i1 = i0 + T < total ? i0 + T : total;
+    a_first = i0 / IPE;
+    a_last = (i1 - 1) / IPE;
+    run_pass = i0 < i1;
+    use_prefetch = false;
+  }
   }
 }
 
@@ -1108,11 +1261,13 @@ __device__ __forceinline__ int xcd_range(int b, int nwg) {
 
 // The decode layer's two streaming GEMMs in one launch: each workgroup
 // runs its gate_up range (FP8: bf16-widened FP8 token rows from the routing
-// launch; W4: bf16 hidden rows -> bf16 SiLU-and-mul rows), then its down
-// range, staging an expert's rows once the gate_up phases that cover the
-// expert reported them (LayerSync).  Every workgroup's gate_up phase runs
-// without waiting, so the waits end as long as the workgroups a wait depends
-// on are resident; a wait that passes kLayerWaitTicks sets ls.err and goes on.
+// launch; W4: bf16 hidden rows -> bf16 SiLU-and-mul rows), then the gate_up
+// ranges it stole (those its down range waits on that nobody had claimed),
+// then its down range, staging an expert's rows once the gate_up work that
+// covers the expert is reported (LayerSync).  No gate_up work ever waits,
+// and every range a down-phase wait depends on is claimed by a running
+// workgroup before the wait begins, so the waits end whatever subset of
+// the workgroups is resident at a time.
 template <int KS1, int KS2, bool W4>
 __global__ __launch_bounds__(W4 ? kCuThreadsW4 : kCuThreads) void stream_layer_kernel(GemmArgs g1, GemmArgs g2,
                                                                                    int cap1, int cap2,
@@ -1137,7 +1292,9 @@ static int run_stream_fp8(const GemmArgs& a, hipStream_t stream) {
   // most four per CU).
   int occ = occupancy_per_cu((const void*)kern, 256, shmem);
   if (occ > kStreamWgPerCu) occ = kStreamWgPerCu;
-  const int grid = occ * device_cu_count();
+  const int cus = device_cu_count();
+  if (occ <= 0 || cus <= 0) return kLaunchError;
+  const int grid = occ * cus;
   kern<<<dim3(grid), dim3(256), shmem, stream>>>(a);
   return launch_status("stream_fp8");
 }
@@ -1147,7 +1304,9 @@ static int run_stream_fp8_cu(const GemmArgs& a, int cap, size_t shmem, hipStream
   auto kern = stream_fp8_cu_kernel<EPI, KS, STAGE>;
   const int st = ensure_dynamic_lds((const void*)kern, shmem, "stream_fp8_cu");
   if (st != kOk) return st;
-  kern<<<dim3(device_cu_count()), dim3(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads), shmem, stream>>>(a, cap);
+  const int cus = device_cu_count();
+  if (cus <= 0) return kLaunchError;
+  kern<<<dim3(cus), dim3(STAGE == STAGE_W4 ? kCuThreadsW4 : kCuThreads), shmem, stream>>>(a, cap);
   return launch_status("stream_fp8_cu");
 }
 
@@ -1211,7 +1370,13 @@ static int run_stream_layer(const GemmArgs& g1, const GemmArgs& g2, LayerSync ls
   auto kern = stream_layer_kernel<KS1, KS2, W4>;
   const int st = ensure_dynamic_lds((const void*)kern, shmem, "stream_layer");
   if (st != kOk) return st;
-  kern<<<dim3(device_cu_count()), dim3(W4 ? kCuThreadsW4 : kCuThreads), shmem, stream>>>(g1, g2, cap1, cap2, ls);
+  const int cus = device_cu_count();
+  if (cus <= 0) return kLaunchError;
+  if (cus > kMaxLayerRanges) {
+    set_last_error("stream_layer: %d CUs, more than the %d claim words of the sync area", cus, kMaxLayerRanges);
+    return kUnsupported;
+  }
+  kern<<<dim3(cus), dim3(W4 ? kCuThreadsW4 : kCuThreads), shmem, stream>>>(g1, g2, cap1, cap2, ls);
   return launch_status("stream_layer");
 }
 
@@ -1232,7 +1397,10 @@ int launch_stream_layer(const GemmArgs& g1, const GemmArgs& g2, bool int4, int* 
   LayerSync ls;
   ls.done = sync_words;
   ls.err = sync_words + g1.num_experts;
+  ls.claim = sync_words + layer_claim_base(g1.num_experts);
   ls.gate_ipe = g1.inter / 8;
+  ls.down_ipe = g2.N / 16;
+  ls.mode = g_layer_test_mode.load(std::memory_order_relaxed);
   if (int4) return run_stream_layer<16, 6, true>(g1, g2, ls, stream);
   return g1.K == 2048 ? run_stream_layer<16, 6, false>(g1, g2, ls, stream)
                       : run_stream_layer<8, 3, false>(g1, g2, ls, stream);

@@ -284,6 +284,7 @@ def fused_experts_op(hidden: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
                      reduce_results: bool, quant: int, w1_scale: Optional[torch.Tensor],
                      w2_scale: Optional[torch.Tensor]) -> torch.Tensor:
     _lib.require_gpu(hidden, w1, w2, topk_weights, topk_ids)
+    hidden = hidden.contiguous()  # the kernels read rows of H elements
     M, H, E, inter = _check_fused_args(hidden, w1, w2, topk_weights, topk_ids, quant, w1_scale, w2_scale)
     top_k = topk_ids.shape[1]
     lib = load()
@@ -320,6 +321,7 @@ def moe_layer(hidden: torch.Tensor, router_logits: torch.Tensor, w1: torch.Tenso
               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Routed MoE layer from router logits: (out, topk_weights fp32, topk_ids int64)."""
     _lib.require_gpu(hidden, router_logits, w1, w2)
+    hidden = hidden.contiguous()
     dummy_ids = torch.empty(hidden.shape[0], top_k, dtype=torch.int64, device=hidden.device)
     dummy_w = torch.empty(hidden.shape[0], top_k, dtype=torch.float32, device=hidden.device)
     M, H, E, inter = _check_fused_args(hidden, w1, w2, dummy_w, dummy_ids, quant, w1_scale, w2_scale)
@@ -356,6 +358,7 @@ def moe_block(hidden: torch.Tensor, gate_weight: torch.Tensor, w1: torch.Tensor,
     """Routed MoE layer from the hidden states (fused router + experts, one
     library call): (out, topk_weights fp32, topk_ids int64)."""
     _lib.require_gpu(hidden, gate_weight, w1, w2)
+    hidden = hidden.contiguous()
     if hidden.dtype != torch.bfloat16 or gate_weight.dtype != torch.bfloat16:
         raise ValueError("moe_block: hidden states and gate weight must be bfloat16")
     dummy_ids = torch.empty(hidden.shape[0], top_k, dtype=torch.int64, device=hidden.device)
