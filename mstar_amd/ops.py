@@ -9,6 +9,7 @@ reference's capture path imposes (mstar/engine/cuda_graph_runner.py:617-640).
 from __future__ import annotations
 
 import ctypes
+import os
 from typing import Optional
 
 import torch
@@ -17,6 +18,38 @@ from . import _lib
 from ._lib import check, dtype_code, load, ptr, stream_of
 
 _NS = "mstar_moe"
+
+
+def _wait_checks_on() -> bool:
+    return os.environ.get("MSTAR_MOE_CHECK_WAITS", "0") not in ("", "0") and \
+        not torch.cuda.is_current_stream_capturing()
+
+
+def _layer_wait_failures() -> int:
+    n = ctypes.c_int(0)
+    check(load().mstar_moe_layer_wait_failures(ctypes.byref(n)), "moe_layer_wait_failures")
+    return n.value
+
+
+def _check_layer_waits(what: str) -> None:
+    """With MSTAR_MOE_CHECK_WAITS=1 in the environment (read per call), an
+    eager layer call synchronises and raises if a wait of the one-launch
+    decode layer kernel gave up during it (its output rows are then NaN);
+    under stream capture there is nothing to read, and the check is skipped.
+    Off by default: it costs a device synchronisation per call."""
+    if not _wait_checks_on():
+        return
+    torch.cuda.synchronize()
+    n = _layer_wait_failures()
+    dev = torch.cuda.current_device()
+    seen = _WAIT_FAILURES.get(dev, n)
+    _WAIT_FAILURES[dev] = n
+    if n > seen:
+        raise _lib.MstarError(f"{what}: {n - seen} wait(s) of the one-launch decode layer gave up "
+                              "(its output is invalid; see mstar_moe_layer_wait_failures)")
+
+
+_WAIT_FAILURES: dict = {}
 
 
 def _on_device(fn):
@@ -335,10 +368,14 @@ def moe_layer(hidden: torch.Tensor, router_logits: torch.Tensor, w1: torch.Tenso
                                              ctypes.byref(nbytes)), "moe_layer")
     ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=hidden.device)
     out = torch.empty(M, H, dtype=hidden.dtype, device=hidden.device)
+    if _wait_checks_on() and torch.cuda.current_device() not in _WAIT_FAILURES:
+        torch.cuda.synchronize()  # the counter before this process's first checked call
+        _WAIT_FAILURES[torch.cuda.current_device()] = _layer_wait_failures()
     check(lib.mstar_moe_layer(
         ptr(hidden), act_dt, M, H, ptr(logits), dtype_code(logits.dtype), int(renormalize), ptr(w1),
         ptr(w2), E, inter, quant, ptr(w1_scale), ptr(w2_scale), top_k, activation, ptr(out),
         ptr(dummy_w), ptr(dummy_ids), ptr(ws), nbytes.value, stream_of(hidden)), "moe_layer")
+    _check_layer_waits("moe_layer")
     return out, dummy_w, dummy_ids
 
 
