@@ -474,17 +474,19 @@ __device__ uint64_t g_timeline[2 * 1024 * 8];  // [EPI][workgroup][phase]
 enum : int { kPhaseAlone = 0, kPhaseGate = 1, kPhaseDown = 2 };
 //
 // Forward progress.  Gate_up range q belongs to whichever workgroup first
-// claims it: claim word q goes 0 -> 1 (its own workgroup, at its start) or
-// 0 -> 2 (a thief).  At the end of its own gate_up phase every workgroup
-// tries to claim each gate_up range its down range depends on and runs the
-// ones it wins before its down phase.  So before any down-phase wait, every
-// range the wait depends on is claimed by a workgroup that is running and
-// whose gate_up work never waits: every wait ends, even when some of the
-// launch's workgroups are not resident (another kernel or process holds CUs)
-// -- the late ones find their ranges taken and go straight to their down
-// work.  A wait longer than kLayerWaitTicks is therefore a fault, not a
-// schedule: it sets *err, counts itself and writes NaN rows for the window it
-// gave up on, so the output is detectably invalid, never silently wrong.
+// claims it: claim word q goes 0 -> 1 (its own workgroup, early in its
+// gate_up phase) or 0 -> 2 (a thief).  Only the claimant reports a range's
+// rows.  At the end of its own gate_up items every workgroup tries to claim
+// each gate_up range its down range depends on and runs the ones it wins
+// before its down phase.  So before any down-phase wait, every range the
+// wait depends on is claimed by a workgroup that is running and whose
+// gate_up work never waits: every wait ends, even when some of the launch's
+// workgroups are not resident (another kernel or process holds CUs).  A late
+// workgroup whose range was taken stops within the unit it is in (rows it
+// wrote get the same values from the thief) and goes on to its down work.  A
+// wait longer than kLayerWaitTicks is therefore a fault, not a schedule: it
+// sets *err, counts itself and writes NaN rows for the window it gave up on,
+// so the output is detectably invalid, never silently wrong.
 enum : int { kLayerNormal = 0, kLayerTestNoOwnClaim = 1, kLayerTestGiveUp = 2 };
 struct LayerSync {
   int* done;       // [E] gate_up (item, token row) pairs finished per expert; zero at launch
@@ -769,7 +771,7 @@ __device__ __forceinline__ void stream_cu_body(const GemmArgs& p, int cap, int w
       for (int qb = dep_lo; qb <= dep_hi && nst < kMaxSteals; qb += 64) {
         const int q = qb + lane;
         int old = 1;
-        if (q <= dep_hi && q != wg) {
+        if (q <= dep_hi) {  // the own range too: it fails unless nobody has claimed it
           old = 0;
           __hip_atomic_compare_exchange_strong(ls.claim + q * kClaimStride, &old, 2, __ATOMIC_RELAXED,
                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
