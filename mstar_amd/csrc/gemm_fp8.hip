@@ -684,6 +684,13 @@ int launch_gemm_fp8_big(const GemmArgs& a, int epi, bool grouped, int bm, hipStr
     set_last_error("gemm_fp8_big: output larger than 4 GiB");
     return kUnsupported;
   }
+  // Every buffer the chosen epilogue writes or the loop reads must exist: a
+  // null output would be written at address 0 by the buffer stores.
+  if (!a.A || !a.B || (!a.cq && !a.C) || (a.pos_of && a.pos_out != 1) || (grouped && (!a.sorted_ids || !a.expert_ids || !a.ntpp)) ||
+      ((grouped || epi == EPI_DENSE) && (!a.a_scale || !a.b_scale))) {
+    set_last_error("gemm_fp8_big: null operand, output or routing table");
+    return kInvalidArgument;
+  }
   if (a.cq && (epi != EPI_ACT || a.inter % 128 != 0 || !a.cs)) {
     set_last_error("gemm_fp8_big: fused quantisation needs the activation epilogue and inter %% 128 == 0");
     return kInvalidArgument;
