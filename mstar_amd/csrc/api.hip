@@ -90,10 +90,10 @@ struct Plan {
 };
 
 // The one-launch decode layer kernel, unless MSTAR_MOE_ONE_LAUNCH=0 in the
-// environment (read once): its workgroups wait on each other, so two such
-// launches must not share a device at the same time; callers that run
-// decode layers concurrently on several streams of one device turn it off
-// and get the two-launch form, which has no such wait.
+// environment (read once).  Its workgroups wait on each other's gate_up
+// work but take over whatever is unclaimed before waiting, so concurrent
+// launches on one device complete; callers that want no cross-workgroup
+// waits at all turn it off and get the two-launch form.
 static bool one_launch_enabled() {
   static const bool on = [] {
     const char* v = getenv("MSTAR_MOE_ONE_LAUNCH");
